@@ -1,0 +1,349 @@
+// C ABI of libevamx: argument validation, workspace layouts and launches (include/evamx.h).
+//
+// Validation mirrors the reference's synchronous checks (csrc/moe_coop3072/moe_coop3072.cu:76-124,
+// moe_coop3072.py:261-297) except the host-synchronising expert bounds check, which becomes a
+// device-side flag (the slot is then treated as inactive, so no pointer outside the table is
+// ever read).
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "evamx_internal.hpp"
+#include "evamx_moe.hpp"
+
+namespace evamx {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+static int rate_k2(float bits)
+{
+    if (!std::isfinite(bits)) return -1;
+    const float k2 = bits * 2.0f;
+    const int i = (int)lrintf(k2);
+    if (std::fabs(k2 - (float)i) > 1e-4f) return -1;
+    if (i >= 2 && i <= 16 && !(i & 1)) return i;           // 1..8
+    if (i == 3 || i == 5 || i == 7) return i;               // 1.5, 2.5, 3.5
+    return -1;
+}
+
+static bool gemv_rate(int k2) { return k2 == 4 || k2 == 6 || k2 == 8 || k2 == 10; }
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct MoeLayout {
+    size_t flags, meta, local, order, runs, chunks, tok_cnt, ctr_gu, ctr_d, rw16, xr, act, part_gu, part_d, total;
+    int slots_max, nslot_max, max_chunks, ks_gu, ks_d;
+};
+
+static int default_ksplit(int work_items, int kt_n, int target)
+{
+    int ks = (target + work_items - 1) / work_items;
+    const int cap = kt_n / 8 < 16 ? kt_n / 8 : 16;
+    if (ks > cap) ks = cap;
+    if (ks < 1) ks = 1;
+    return ks;
+}
+
+static bool shape_ok(const evamx_moe_shape* s)
+{
+    if (!s) { set_error("evamx: null shape"); return false; }
+    if (s->rows_max < 1 || s->rows_max > 65536) { set_error("evamx: rows_max %d outside 1..65536", s->rows_max); return false; }
+    if (s->hidden < 128 || s->hidden % 128 || s->inter < 128 || s->inter % 128) {
+        set_error("evamx: hidden %d and inter %d must be positive multiples of 128", s->hidden, s->inter);
+        return false;
+    }
+    if (s->topk < 1 || s->topk > EVAMX_MAX_TOPK) { set_error("evamx: topk %d outside 1..%d", s->topk, EVAMX_MAX_TOPK); return false; }
+    if (s->n_local < 1 || s->n_local > EVAMX_MAX_EXPERTS) {
+        set_error("evamx: n_local %d outside 1..%d", s->n_local, EVAMX_MAX_EXPERTS);
+        return false;
+    }
+    if (s->ksplit_gu < 0 || s->ksplit_gu > 64 || s->ksplit_down < 0 || s->ksplit_down > 64) {
+        set_error("evamx: ksplit outside 0..64");
+        return false;
+    }
+    if ((long)s->rows_max * s->topk > 65536) { set_error("evamx: rows_max*topk above 65536"); return false; }
+    return true;
+}
+
+static MoeLayout moe_layout(const evamx_moe_shape* s)
+{
+    MoeLayout L;
+    L.slots_max = s->rows_max * s->topk;
+    L.nslot_max = L.slots_max + (s->has_shared ? s->rows_max : 0);
+    const int routed_chunks = (L.slots_max < s->n_local ? L.slots_max : s->n_local) + L.slots_max / EVAMX_CHUNK;
+    L.max_chunks = routed_chunks + (s->has_shared ? (s->rows_max + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
+    const int chunks_est = (L.slots_max < s->n_local ? L.slots_max : s->n_local) + (s->has_shared ? 1 : 0);
+    L.ks_gu = s->ksplit_gu ? s->ksplit_gu : default_ksplit(chunks_est * 2 * (s->inter / 128), s->hidden / 16, 2048);
+    L.ks_d = s->ksplit_down ? s->ksplit_down : default_ksplit(chunks_est * (s->hidden / 128), s->inter / 16, 2048);
+    size_t o = 0;
+    L.flags = o;   o = al256(o + 64 * 4);
+    L.meta = o;    o = al256(o + 64 * 4);
+    L.local = o;   o = al256(o + (size_t)L.slots_max * 4);
+    L.order = o;   o = al256(o + (size_t)L.nslot_max * 4);
+    L.runs = o;    o = al256(o + (size_t)(2 + 2 * L.slots_max + 1) * 4);
+    L.chunks = o;  o = al256(o + (size_t)L.max_chunks * 16);
+    L.tok_cnt = o; o = al256(o + (size_t)s->rows_max * 4);
+    L.ctr_gu = o;  o = al256(o + (size_t)L.max_chunks * (s->inter / 128) * 4);
+    L.ctr_d = o;   o = al256(o + (size_t)s->rows_max * (s->hidden / 128) * 4);
+    L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
+    L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
+    L.act = o;     o = al256(o + (size_t)L.nslot_max * s->inter * 2);
+    L.part_gu = o; o = al256(o + (size_t)L.ks_gu * 2 * L.nslot_max * s->inter * 4);
+    L.part_d = o;  o = al256(o + (size_t)L.ks_d * L.nslot_max * s->hidden * 4);
+    L.total = o;
+    return L;
+}
+
+__global__ void fill_i32_kernel(int* p, int n, int v)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+static int launched(const char* what)
+{
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("evamx: %s launch failed: %s", what, hipGetErrorString(e));
+        return EVAMX_ELAUNCH;
+    }
+    return EVAMX_OK;
+}
+
+}  // namespace evamx
+
+using namespace evamx;
+
+#define EVAMX_REQUIRE(cond, ...)              \
+    do {                                      \
+        if (!(cond)) {                        \
+            set_error(__VA_ARGS__);           \
+            return EVAMX_EINVAL;              \
+        }                                     \
+    } while (0)
+
+extern "C" const char* evamx_last_error(void) { return g_err; }
+
+extern "C" int evamx_abi_version(void) { return 1; }
+
+extern "C" int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, float bits, void* w_fp16,
+                                  evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    const int k2 = rate_k2(bits);
+    EVAMX_REQUIRE(trellis && w_fp16, "evamx_exl3_dequant: null pointer");
+    EVAMX_REQUIRE(k2 > 0, "evamx_exl3_dequant: unsupported bit rate %g", (double)bits);
+    EVAMX_REQUIRE(in_features >= 16 && out_features >= 16 && in_features % 16 == 0 && out_features % 16 == 0,
+                  "evamx_exl3_dequant: in/out (%d, %d) must be positive multiples of 16", in_features, out_features);
+    launch_dequant(trellis, in_features, out_features, k2, w_fp16, false, (hipStream_t)stream);
+    return launched("dequant");
+}
+
+extern "C" size_t evamx_exl3_linear_workspace_bytes(int rows, int in_features, int out_features)
+{
+    if (rows < 1 || in_features < 128 || out_features < 128) return 0;
+    return linear_workspace(rows, in_features, out_features, nullptr, nullptr);
+}
+
+extern "C" int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, int out_features, const void* trellis,
+                                 const void* suh_fp16, const void* svh_fp16, float bits, void* y_fp16, void* workspace,
+                                 size_t workspace_bytes, evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    const int k2 = rate_k2(bits);
+    EVAMX_REQUIRE(x_fp16 && trellis && suh_fp16 && svh_fp16 && y_fp16 && workspace, "evamx_exl3_linear: null pointer");
+    EVAMX_REQUIRE(rows >= 1 && rows <= 16, "evamx_exl3_linear: rows %d outside 1..16", rows);
+    EVAMX_REQUIRE(in_features >= 128 && out_features >= 128 && in_features % 128 == 0 && out_features % 128 == 0,
+                  "evamx_exl3_linear: in/out (%d, %d) must be positive multiples of 128", in_features, out_features);
+    EVAMX_REQUIRE(gemv_rate(k2), "evamx_exl3_linear: bit rate %g not in {2,3,4,5}", (double)bits);
+    const size_t need = linear_workspace(rows, in_features, out_features, nullptr, nullptr);
+    if (workspace_bytes < need) {
+        set_error("evamx_exl3_linear: workspace %zu bytes < %zu", workspace_bytes, need);
+        return EVAMX_ENOSPACE;
+    }
+    launch_linear(x_fp16, rows, in_features, out_features, trellis, suh_fp16, svh_fp16, k2, y_fp16, workspace,
+                  (hipStream_t)stream);
+    return launched("linear");
+}
+
+extern "C" int evamx_route_topk(const float* logits, const float* sel_bias, int rows, int n_experts, int topk,
+                                int score_fn, float route_scale, int64_t* indices, float* weights, void* rw_fp16,
+                                evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    EVAMX_REQUIRE(logits && indices && weights && rw_fp16, "evamx_route_topk: null pointer");
+    EVAMX_REQUIRE(rows >= 1 && rows <= 65536, "evamx_route_topk: rows %d outside 1..65536", rows);
+    EVAMX_REQUIRE(n_experts >= 1 && n_experts <= EVAMX_MAX_EXPERTS, "evamx_route_topk: n_experts %d outside 1..%d",
+                  n_experts, EVAMX_MAX_EXPERTS);
+    EVAMX_REQUIRE(topk >= 1 && topk <= EVAMX_MAX_TOPK && topk <= n_experts, "evamx_route_topk: topk %d invalid", topk);
+    EVAMX_REQUIRE(score_fn == EVAMX_SCORE_SIGMOID || score_fn == EVAMX_SCORE_SQRT_SOFTPLUS,
+                  "evamx_route_topk: unknown score function %d", score_fn);
+    EVAMX_REQUIRE(std::isfinite(route_scale), "evamx_route_topk: route_scale must be finite");
+    MoeParams p;
+    memset(&p, 0, sizeof p);
+    p.mode = 0;
+    p.T = rows; p.topk = topk; p.n_logits = n_experts;
+    p.logits = logits; p.sel_bias = sel_bias; p.score = score_fn; p.route_scale = route_scale;
+    p.sel = indices; p.weights = weights; p.rw16 = (half_t*)rw_fp16;
+    moe_prepare_only(p, (hipStream_t)stream);
+    return launched("route_topk");
+}
+
+extern "C" size_t evamx_prepare_routes_workspace_bytes(int capacity, int topk)
+{
+    if (capacity < 1 || topk < 1) return 0;
+    return 256 + al256((size_t)capacity * topk * 4);
+}
+
+extern "C" int32_t* evamx_prepare_routes_flags_ptr(void* workspace) { return (int32_t*)workspace; }
+
+extern "C" int evamx_prepare_routes(const int64_t* sel, const void* rw_fp16, int rows, int topk, int capacity,
+                                    int n_local, int32_t* runs, void* workspace, size_t workspace_bytes,
+                                    evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    EVAMX_REQUIRE(sel && rw_fp16 && runs && workspace, "evamx_prepare_routes: null pointer");
+    EVAMX_REQUIRE(topk >= 1 && topk <= EVAMX_MAX_TOPK, "evamx_prepare_routes: topk %d outside 1..%d", topk, EVAMX_MAX_TOPK);
+    EVAMX_REQUIRE(capacity >= 1 && (long)capacity * topk <= 65536, "evamx_prepare_routes: capacity %d invalid", capacity);
+    EVAMX_REQUIRE(rows >= 1 && rows <= capacity, "evamx_prepare_routes: rows %d outside 1..capacity", rows);
+    EVAMX_REQUIRE(n_local >= 1 && n_local <= EVAMX_MAX_EXPERTS, "evamx_prepare_routes: n_local %d outside 1..%d",
+                  n_local, EVAMX_MAX_EXPERTS);
+    const size_t need = evamx_prepare_routes_workspace_bytes(capacity, topk);
+    if (workspace_bytes < need) {
+        set_error("evamx_prepare_routes: workspace %zu bytes < %zu", workspace_bytes, need);
+        return EVAMX_ENOSPACE;
+    }
+    MoeParams p;
+    memset(&p, 0, sizeof p);
+    p.mode = PREP_GROUP;
+    p.T = rows; p.topk = topk; p.n_local = n_local;
+    p.sel = const_cast<int64_t*>(sel);
+    p.rw16 = (half_t*)const_cast<void*>(rw_fp16);
+    p.min_expert = -1;
+    p.err = (int*)workspace;
+    p.local = (int*)((char*)workspace + 256);
+    p.runs = runs;
+    p.slots_max = capacity * topk;
+    moe_prepare_only(p, (hipStream_t)stream);
+    return launched("prepare_routes");
+}
+
+extern "C" size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape)
+{
+    if (!shape_ok(shape)) return 0;
+    return moe_layout(shape).total;
+}
+
+extern "C" int32_t* evamx_moe_runs_ptr(const evamx_moe_shape* shape, void* workspace)
+{
+    if (!shape_ok(shape) || !workspace) return nullptr;
+    return (int32_t*)((char*)workspace + moe_layout(shape).runs);
+}
+
+extern "C" int32_t* evamx_moe_flags_ptr(const evamx_moe_shape* shape, void* workspace)
+{
+    if (!shape_ok(shape) || !workspace) return nullptr;
+    return (int32_t*)((char*)workspace + moe_layout(shape).flags);
+}
+
+extern "C" int evamx_moe_workspace_init(const evamx_moe_shape* shape, void* workspace, evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    if (!shape_ok(shape)) return EVAMX_EINVAL;
+    EVAMX_REQUIRE(workspace, "evamx_moe_workspace_init: null workspace");
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                       (int*)((char*)workspace + moe_layout(shape).flags), 64, 0);
+    return launched("workspace_init");
+}
+
+extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    EVAMX_REQUIRE(a, "evamx_moe_forward: null args");
+    const evamx_moe_shape* s = &a->shape;
+    if (!shape_ok(s)) return EVAMX_EINVAL;
+    const MoeLayout L = moe_layout(s);
+    EVAMX_REQUIRE(a->rows >= 1 && a->rows <= s->rows_max, "evamx_moe_forward: rows %d outside 1..%d", a->rows, s->rows_max);
+    EVAMX_REQUIRE(a->x && a->out && a->tables && a->sel && a->workspace, "evamx_moe_forward: null pointer");
+    EVAMX_REQUIRE(a->x_dtype == EVAMX_DTYPE_F16 || a->x_dtype == EVAMX_DTYPE_BF16, "evamx_moe_forward: x_dtype %d", a->x_dtype);
+    EVAMX_REQUIRE(a->x_stride >= s->hidden && a->out_stride >= s->hidden, "evamx_moe_forward: row strides below hidden");
+    EVAMX_REQUIRE(std::isfinite(a->limit) && a->limit >= 0.0f, "evamx_moe_forward: limit must be finite and >= 0");
+    if (a->logits) {
+        EVAMX_REQUIRE(a->n_logits >= s->topk && a->n_logits <= EVAMX_MAX_EXPERTS,
+                      "evamx_moe_forward: n_logits %d must be in topk..%d", a->n_logits, EVAMX_MAX_EXPERTS);
+        EVAMX_REQUIRE(a->weights, "evamx_moe_forward: routing needs a weights output");
+        EVAMX_REQUIRE(a->score_fn == EVAMX_SCORE_SIGMOID || a->score_fn == EVAMX_SCORE_SQRT_SOFTPLUS,
+                      "evamx_moe_forward: unknown score function %d", a->score_fn);
+        EVAMX_REQUIRE(std::isfinite(a->route_scale), "evamx_moe_forward: route_scale must be finite");
+    } else {
+        EVAMX_REQUIRE(a->weights || a->rw_fp16, "evamx_moe_forward: routes need fp32 weights or fp16 rw");
+    }
+    if (a->min_expert >= 0)
+        EVAMX_REQUIRE(a->max_expert > a->min_expert, "evamx_moe_forward: empty expert range");
+    int k2u = 0;
+    if (!a->k2_per_expert) {
+        k2u = rate_k2(a->bits);
+        EVAMX_REQUIRE(gemv_rate(k2u), "evamx_moe_forward: bit rate %g not in {2,3,4,5}", (double)a->bits);
+    }
+    int k2s = 0;
+    if (s->has_shared) {
+        EVAMX_REQUIRE(a->shared, "evamx_moe_forward: shape has a shared expert but no pointers were given");
+        for (int i = 0; i < 9; ++i) EVAMX_REQUIRE(a->shared[i] != 0, "evamx_moe_forward: shared pointer %d is null", i);
+        k2s = rate_k2(a->shared_bits);
+        EVAMX_REQUIRE(gemv_rate(k2s), "evamx_moe_forward: shared bit rate %g not in {2,3,4,5}", (double)a->shared_bits);
+    }
+    if (a->workspace_bytes < L.total) {
+        set_error("evamx_moe_forward: workspace %zu bytes < %zu", a->workspace_bytes, L.total);
+        return EVAMX_ENOSPACE;
+    }
+
+    char* ws = (char*)a->workspace;
+    MoeParams p;
+    memset(&p, 0, sizeof p);
+    p.mode = PREP_GROUP | PREP_MOE;
+    p.T = a->rows; p.H = s->hidden; p.I = s->inter; p.topk = s->topk; p.n_local = s->n_local;
+    p.n_logits = a->n_logits;
+    p.x = a->x; p.x_dtype = a->x_dtype; p.x_stride = a->x_stride;
+    p.logits = a->logits; p.sel_bias = a->sel_bias; p.score = a->score_fn; p.route_scale = a->route_scale;
+    p.sel = a->sel;
+    p.weights = a->weights;
+    p.rw16 = a->rw_fp16 ? (half_t*)a->rw_fp16 : (half_t*)(ws + L.rw16);
+    if (!a->logits && !a->weights) p.weights = nullptr;    // rw_fp16 is the input
+    p.min_expert = a->min_expert >= 0 ? a->min_expert : -1;
+    p.max_expert = a->max_expert;
+    p.tables = a->tables; p.tbl_stride = s->n_local;
+    p.k2_per_expert = a->k2_per_expert; p.k2_uniform = k2u; p.k2_shared = k2s;
+    p.has_shared = s->has_shared ? 1 : 0;
+    if (s->has_shared)
+        for (int i = 0; i < 9; ++i) p.sh_ptr[i] = a->shared[i];
+    p.limit = a->limit;
+    p.err = (int*)(ws + L.flags);
+    p.meta = (int*)(ws + L.meta);
+    p.local = (int*)(ws + L.local);
+    p.order = (int*)(ws + L.order);
+    p.runs = (int*)(ws + L.runs);
+    p.slots_max = L.slots_max;
+    p.chunks = (int*)(ws + L.chunks);
+    p.max_chunks = L.max_chunks;
+    p.tok_cnt = (int*)(ws + L.tok_cnt);
+    p.ctr_gu = (int*)(ws + L.ctr_gu); p.ctr_gu_len = L.max_chunks * (s->inter / 128);
+    p.ctr_d = (int*)(ws + L.ctr_d); p.ctr_d_len = s->rows_max * (s->hidden / 128);
+    p.xr = (half_t*)(ws + L.xr);
+    p.act = (half_t*)(ws + L.act);
+    p.part_gu = (float*)(ws + L.part_gu);
+    p.part_d = (float*)(ws + L.part_d);
+    p.nslot_max = L.nslot_max;
+    p.ks_gu = L.ks_gu; p.ks_d = L.ks_d;
+    p.out = a->out; p.out_stride = a->out_stride;
+    moe_launch(p, (hipStream_t)stream);
+    return launched("moe_forward");
+}

@@ -1,0 +1,134 @@
+// Device-side building blocks for the EXL3 MoE path on gfx950 (wave64).
+//
+// Trellis format and codebook: runtime/ds41/csrc/moe_coop3072/vendor/quant/exl3_dq.cuh:15-31
+// (bit windows), codebook.cuh:86-99 (MUL1 decode). Hadamard evaluation order:
+// hadamard_inner.cuh:17-44 and exl3_moe_coop_kernel.cuh:131-147.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace evamx {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+constexpr float R_SCALE = 0.088388347648f;   // 1/sqrt(128) as the reference spells it
+
+__device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, int s)
+{
+    // ((hi:lo) >> s) low 32 bits; s is a compile-time constant at every call site (v_alignbit)
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> s);
+}
+
+// MUL1 hash of a 16-bit state sitting in the low (HI=false) or high (HI=true) half of r:
+// state * 0x83DCD12D mod 2^32, split as state*0xD12D + ((state*0x83DC) mod 2^16) << 16 so that
+// it maps to a 16-bit multiply with a word-1 destination (SDWA) and a 16x16->32 multiply-add,
+// instead of the multi-pass 32-bit multiply.
+// Written in inline asm: the compiler otherwise folds the split back into v_mul_lo_u32, or
+// masks the half with an extra instruction instead of using the 16-bit operand selects.
+template <bool HI>
+__device__ __forceinline__ uint32_t mul1_hash(uint32_t r)
+{
+    uint32_t y, p;
+    if constexpr (HI) {
+        asm("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
+            : "=v"(y) : "v"(r), "v"(0x83DCu));
+        asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(r), "v"(0xD12Du), "v"(y));
+    } else {
+        asm("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+            : "=v"(y) : "v"(r), "v"(0x83DCu));
+        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(r), "v"(0xD12Du), "v"(y));
+    }
+    return p;
+}
+
+// Two decoded weights (fp16, bit-exact MUL1 decode) from two hashes:
+// h = fp16_bits(0x6400 + bytesum) = 1024 + bytesum, w = fma_fp16(h, 0x1eee, 0xc931).
+__device__ __forceinline__ half2_t mul1_pair(uint32_t p0, uint32_t p1)
+{
+    uint32_t s = __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u);
+    s = __builtin_amdgcn_sad_hi_u8(p1, 0u, s);
+    const half2_t h = __builtin_bit_cast(half2_t, s);
+    const half2_t k = {__builtin_bit_cast(half_t, (uint16_t)0x1eee), __builtin_bit_cast(half_t, (uint16_t)0x1eee)};
+    const half2_t b = {__builtin_bit_cast(half_t, (uint16_t)0xc931), __builtin_bit_cast(half_t, (uint16_t)0xc931)};
+    return __builtin_elementwise_fma(h, k, b);
+}
+
+__device__ __forceinline__ half_t mul1_one(uint32_t state)
+{
+    const half2_t w = mul1_pair(mul1_hash<false>(state), 0u);
+    return w.x;
+}
+
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c)
+{
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Lane-local window geometry.
+//
+// A lane owns 32 consecutive positions of a 16x16 tile: the positions of reference lanes
+// 4q..4q+3 (q = lane % 8), i.e. columns q and q+8 for all 16 k of the tile. For an integer
+// rate K those positions end inside the lane's K words, and the first windows reach back
+// into the previous word (the last word of lane q-1 of the same tile, circularly). The bit
+// string B = prev:W0:...:W(K-1) (MSB first) holds position j's window at bits
+// [E(j)-16, E(j)) with E(j) = 32 + (j+1)K.
+
+template <int K>
+struct LaneWords {
+    uint32_t b[K + 1];   // b[0] = previous word, b[1..K] = own words
+};
+
+template <int K>
+__device__ __forceinline__ constexpr int win_end(int j) { return 32 + (j + 1) * K; }
+
+// Register whose low 16 bits are the window ending at E (and whose high 16 bits are the
+// window ending at E-16).
+template <int K, int E>
+__device__ __forceinline__ uint32_t win_reg(const LaneWords<K>& w)
+{
+    constexpr int L = (E - 1) / 32;
+    constexpr int S = 32 * (L + 1) - E;
+    static_assert(L >= 1 && L <= K, "window outside the lane's words");
+    return funnel(w.b[L - 1], w.b[L], S);
+}
+
+// Hash of lane-local position j (0..31). When the window 16 bits later is also in range
+// (K divides 16), the window sits in the high half of that window's register, so pairs
+// share one funnel shift.
+template <int K, int J>
+__device__ __forceinline__ uint32_t lane_hash(const LaneWords<K>& w)
+{
+    constexpr int E = win_end<K>(J);
+    constexpr bool SHARE = (16 % K == 0) && (J + 16 / K) < 32;
+    if constexpr (SHARE)
+        return mul1_hash<true>(win_reg<K, E + 16>(w));
+    else
+        return mul1_hash<false>(win_reg<K, E>(w));
+}
+
+// Decoded weight pair of lane-local positions (J, J+1) (J even): same column, k and k+1.
+template <int K, int J>
+__device__ __forceinline__ half2_t lane_pair(const LaneWords<K>& w)
+{
+    return mul1_pair(lane_hash<K, J>(w), lane_hash<K, J + 1>(w));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wave-level 128-point Hadamard in the reference's fp32 evaluation order: radix-2 on element
+// bits 0..6 in increasing order, lower index a+b, upper a-b, scale last. Bit-identical to the
+// reference for any data layout, because IEEE addition is commutative and each stage's
+// operand pairs are the same.
+
+// Butterfly where the partner lives in another lane (lane ^ m); `upper` = this lane holds the
+// element with the stage bit set.
+__device__ __forceinline__ float bfly_x(float v, int m, bool upper)
+{
+    const float p = __shfl_xor(v, m, WAVE);
+    return upper ? (p - v) : (v + p);
+}
+
+}  // namespace evamx

@@ -1,0 +1,72 @@
+// Kernel parameter block of the decode MoE pipeline (device pointers into the caller's
+// workspace, see moe_workspace_layout in capi.hip).
+#pragma once
+#include <stdint.h>
+#include "../../include/evamx.h"
+#include "evamx_device.hpp"
+
+namespace evamx {
+
+constexpr int EVAMX_MAX_EXPERTS = 512;     // pointer-table entries per layer (reference: <= 384)
+constexpr int EVAMX_MAX_TOPK = 32;         // reference bound: top_k <= 32 (exl3_moe_coop_kernel.cuh:46)
+constexpr int EVAMX_CHUNK = 16;            // slots of one expert per GEMV work item
+
+// Pointer-table rows, in the reference's order (ds41/cache.py:1877-1886).
+enum {
+    EVAMX_TBL_G_TRELLIS = 0, EVAMX_TBL_G_SUH = 1, EVAMX_TBL_G_SVH = 2,
+    EVAMX_TBL_U_TRELLIS = 3, EVAMX_TBL_U_SUH = 4, EVAMX_TBL_U_SVH = 5,
+    EVAMX_TBL_D_TRELLIS = 6, EVAMX_TBL_D_SUH = 7, EVAMX_TBL_D_SVH = 8,
+};
+
+enum { PREP_GROUP = 1, PREP_MOE = 2 };
+
+struct MoeParams {
+    int mode;
+    int T, H, I, topk, n_local, n_logits;
+    // input rows
+    const void* x;
+    int x_dtype, x_stride;
+    // routing
+    const float* logits;
+    const float* sel_bias;
+    int score;
+    float route_scale;
+    int64_t* sel;
+    float* weights;            // fp32 weights: output when routing, input otherwise (null: rw16 given)
+    half_t* rw16;
+    int min_expert, max_expert;
+    // experts
+    const int64_t* tables;     // [9][tbl_stride]
+    int tbl_stride;
+    const uint8_t* k2_per_expert;
+    int k2_uniform, k2_shared;
+    int has_shared;
+    int64_t sh_ptr[9];
+    float limit;
+    // workspace
+    int* err;
+    int* local;                // [slots]
+    int* order;                // [slots + T]
+    int* runs;                 // reference run table [2 + 2*slots_max + 1]
+    int slots_max;
+    int* chunks;               // [max_chunks][4]: expert (-1 shared), begin, count, k2
+    int max_chunks;
+    int* meta;                 // [0] n_chunks, [1] n_active
+    int* ctr_gu; int ctr_gu_len;
+    int* ctr_d; int ctr_d_len;
+    int* tok_cnt;              // [T]
+    half_t* xr;                // [2][nslot_max][H]
+    half_t* act;               // [nslot_max][I]
+    float* part_gu;            // [ks_gu][2][nslot_max][I]
+    float* part_d;             // [ks_d][nslot_max][H]
+    int nslot_max;
+    int ks_gu, ks_d;
+    // output
+    float* out;
+    int out_stride;
+};
+
+int moe_launch(MoeParams& p, hipStream_t stream);
+int moe_prepare_only(MoeParams& p, hipStream_t stream);
+
+}  // namespace evamx

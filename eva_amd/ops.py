@@ -1,0 +1,184 @@
+"""Tensor-level wrappers of the evamx C ABI (PyTorch-ROCm tensors in, device pointers out).
+
+Every function launches HIP kernels from libevamx.so on the current stream; nothing here
+computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import MoeArgs, MoeShape, check, lib, ptr, stream_handle
+
+SCORE_FNS = {"sigmoid": _lib.SCORE_SIGMOID, "sqrt_softplus": _lib.SCORE_SQRT_SOFTPLUS}
+RATES = (2.0, 3.0, 4.0, 5.0)
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None, ndim=None):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.ndim != ndim:
+        raise ValueError(f"{name} must have {ndim} dims")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def tile_u16(bits: float) -> int:
+    b = float(bits)
+    return 16 * int(b) + 8 if b != int(b) else 16 * int(b)
+
+
+def exl3_dequant(trellis: torch.Tensor, bits: float) -> torch.Tensor:
+    """fp16 ``W[in][out]`` of an EXL3 projection ``trellis int16 [in/16, out/16, T]``."""
+    _dev(trellis, "trellis", torch.int16, 3)
+    kt, nt, t16 = trellis.shape
+    if t16 != tile_u16(bits):
+        raise ValueError(f"trellis last dim {t16} does not match {bits} bits")
+    w = torch.empty(kt * 16, nt * 16, dtype=torch.float16, device=trellis.device)
+    check(lib().evamx_exl3_dequant(ptr(trellis), kt * 16, nt * 16, float(bits), ptr(w),
+                                   stream_handle(trellis.device)), "evamx_exl3_dequant")
+    return w
+
+
+def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bits: float,
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Single EXL3 linear, fp16 ``x [M, in]`` (M <= 16) -> fp16 ``[M, out]``."""
+    _dev(x, "x", torch.float16, 2)
+    _dev(trellis, "trellis", torch.int16, 3)
+    _dev(suh, "suh", torch.float16, 1)
+    _dev(svh, "svh", torch.float16, 1)
+    m, n_in = x.shape
+    n_out = svh.numel()
+    if suh.numel() != n_in or trellis.shape[0] * 16 != n_in or trellis.shape[1] * 16 != n_out:
+        raise ValueError("x / trellis / suh / svh shapes disagree")
+    if out is None:
+        out = torch.empty(m, n_out, dtype=torch.float16, device=x.device)
+    need = lib().evamx_exl3_linear_workspace_bytes(m, n_in, n_out)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    check(lib().evamx_exl3_linear(ptr(x), m, n_in, n_out, ptr(trellis), ptr(suh), ptr(svh), float(bits), ptr(out),
+                                  ptr(workspace), workspace.numel(), stream_handle(x.device)), "evamx_exl3_linear")
+    return out
+
+
+def route_topk(logits: torch.Tensor, topk: int, score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None,
+               route_scale: float = 1.0):
+    """(indices int64, weights fp32, rw fp16) of the top-k experts per row of ``logits [T, E]``."""
+    _dev(logits, "logits", torch.float32, 2)
+    t, e = logits.shape
+    if sel_bias is not None:
+        _dev(sel_bias, "sel_bias", torch.float32, 1)
+    idx = torch.empty(t, topk, dtype=torch.int64, device=logits.device)
+    w = torch.empty(t, topk, dtype=torch.float32, device=logits.device)
+    rw = torch.empty(t, topk, dtype=torch.float16, device=logits.device)
+    check(lib().evamx_route_topk(ptr(logits), ptr(sel_bias), t, e, topk, SCORE_FNS[score_fn], float(route_scale),
+                                 ptr(idx), ptr(w), ptr(rw), stream_handle(logits.device)), "evamx_route_topk")
+    return idx, w, rw
+
+
+def prepare_routes(sel: torch.Tensor, rw: torch.Tensor, capacity: int, n_local: int,
+                   runs: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference run table ``int32 [2 + 2*capacity*topk + 1]`` for routes ``sel``/``rw`` (fp16)."""
+    _dev(sel, "sel", torch.int64, 2)
+    _dev(rw, "rw", torch.float16, 2)
+    t, k = sel.shape
+    if rw.shape != sel.shape:
+        raise ValueError("sel/rw shapes differ")
+    if runs is None:
+        runs = torch.empty(2 + 2 * capacity * k + 1, dtype=torch.int32, device=sel.device)
+    need = lib().evamx_prepare_routes_workspace_bytes(capacity, k)
+    if workspace is None:
+        workspace = torch.zeros(need, dtype=torch.uint8, device=sel.device)
+    check(lib().evamx_prepare_routes(ptr(sel), ptr(rw), t, k, capacity, n_local, ptr(runs), ptr(workspace),
+                                     workspace.numel(), stream_handle(sel.device)), "evamx_prepare_routes")
+    return runs
+
+
+class MoeWorkspace:
+    """Device workspace of the MoE forward for one shape (owned by one runner)."""
+
+    def __init__(self, device, rows_max: int, hidden: int, inter: int, topk: int, n_local: int,
+                 has_shared: bool, ksplit_gu: int = 0, ksplit_down: int = 0):
+        self.shape = MoeShape(rows_max, hidden, inter, topk, n_local, int(bool(has_shared)), ksplit_gu, ksplit_down)
+        nbytes = lib().evamx_moe_workspace_bytes(ctypes.byref(self.shape))
+        if nbytes == 0:
+            raise ValueError("invalid MoE shape: " + lib().evamx_last_error().decode())
+        self.device = torch.device(device)
+        self.buffer = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        check(lib().evamx_moe_workspace_init(ctypes.byref(self.shape), ptr(self.buffer), stream_handle(self.device)),
+              "evamx_moe_workspace_init")
+
+    def runs(self) -> torch.Tensor:
+        """View of the run table written by the last forward."""
+        slots = self.shape.rows_max * self.shape.topk
+        addr = lib().evamx_moe_runs_ptr(ctypes.byref(self.shape), ptr(self.buffer))
+        off = addr - self.buffer.data_ptr()
+        n = 2 + 2 * slots + 1
+        return self.buffer[off:off + 4 * n].view(torch.int32)
+
+    def flags(self) -> torch.Tensor:
+        addr = lib().evamx_moe_flags_ptr(ctypes.byref(self.shape), ptr(self.buffer))
+        off = addr - self.buffer.data_ptr()
+        return self.buffer[off:off + 4].view(torch.int32)
+
+
+def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: torch.Tensor, *, limit: float,
+                bits: float | None = None, k2_per_expert: torch.Tensor | None = None,
+                logits: torch.Tensor | None = None, sel: torch.Tensor | None = None,
+                weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
+                score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
+                shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0):
+    """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
+
+    With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
+    must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
+    the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
+    """
+    s = ws.shape
+    _dev(x, "x", None, 2)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("x must be fp16 or bf16")
+    _dev(tables, "tables", torch.int64, 2)
+    _dev(out, "out", torch.float32, 2)
+    if tables.shape != (9, s.n_local):
+        raise ValueError(f"tables must be [9, {s.n_local}]")
+    rows = x.shape[0]
+    a = MoeArgs()
+    a.shape = s
+    a.rows = rows
+    a.x = ptr(x)
+    a.x_dtype = _lib.DTYPE_F16 if x.dtype == torch.float16 else _lib.DTYPE_BF16
+    a.x_stride = x.stride(0)
+    if logits is not None:
+        _dev(logits, "logits", torch.float32, 2)
+        a.logits = ptr(logits)
+        a.n_logits = logits.shape[1]
+        a.sel_bias = ptr(sel_bias)
+        a.score_fn = SCORE_FNS[score_fn]
+        a.route_scale = float(route_scale)
+    a.sel = ptr(sel)
+    a.weights = ptr(weights)
+    a.rw_fp16 = ptr(rw)
+    a.min_expert = min_expert
+    a.max_expert = max_expert
+    a.tables = ptr(tables)
+    a.k2_per_expert = ptr(k2_per_expert)
+    a.bits = float(bits) if bits is not None else 0.0
+    keep = None
+    if shared_ptrs is not None:
+        keep = (ctypes.c_int64 * 9)(*[int(v) for v in shared_ptrs])
+        a.shared = ctypes.cast(keep, ctypes.c_void_p)
+        a.shared_bits = float(shared_bits)
+    a.limit = float(limit)
+    a.out = ptr(out)
+    a.out_stride = out.stride(0)
+    a.workspace = ptr(ws.buffer)
+    a.workspace_bytes = ws.buffer.numel()
+    check(lib().evamx_moe_forward(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward")
+    del keep
+    return out

@@ -1,0 +1,151 @@
+/*
+ * evamx: MI355X (gfx950) implementation of eva's cooperative EXL3 MoE expert path, as a
+ * C ABI. Plain pointers and sizes; every pointer argument documented "device" is a HIP device
+ * pointer; `stream` is a hipStream_t. No entry point allocates or synchronises with the host,
+ * so a forward call can be captured into a hipGraph. Errors are returned as negative codes
+ * with a message from evamx_last_error() (thread-local).
+ *
+ * Reference interfaces replaced (paths under runtime/ds41/ of the eva repository):
+ *   evamx_exl3_dequant       decoded fp16 weights of an EXL3 projection:
+ *                            csrc/moe_coop3072/vendor/quant/exl3_dq.cuh:96-330 with
+ *                            codebook.cuh:86-99 (the "decoded fp16 weight" contract)
+ *   evamx_exl3_linear        ELinear.forward -> LinearEXL3 (exl3_linear.py:97-131,134-154),
+ *                            kernel csrc/moe_coop3072/vendor/quant/exl3_gemv_kernel.cuh:195-491
+ *   evamx_route_topk         Block.route (model.py:404-416) with the stable tie rule of
+ *                            _stable_topk_indices (model.py:940-953)
+ *   evamx_prepare_routes     CoopRunner3072.prepare_routes -> pybind prepare_routes
+ *                            (moe_coop3072.py:321-358; csrc/moe_coop3072/moe_coop3072.cu:149-174)
+ *   evamx_moe_forward        CoopRunner*.run -> pybind run / exllamav3_ext.exl3_moe_coop
+ *                            (moe_coop.py:42-69; moe_coop3072.py:261-319;
+ *                            csrc/moe_coop3072/moe_coop3072.cu:73-145;
+ *                            csrc/moe_coop3072/vendor/quant/exl3_moe_coop.cuh:115-152),
+ *                            plus the shared expert added by Block.experts (model.py:418-452,498)
+ *   evamx_moe_workspace_bytes  WorkspaceLayout.scratch_bytes / exl3_moe_coop_ctr_len
+ *                            (moe_coop3072.py:120-152; exl3_moe_coop.cuh:154-159)
+ */
+#ifndef EVAMX_H
+#define EVAMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* evamx_stream_t; /* hipStream_t */
+
+enum { EVAMX_OK = 0, EVAMX_EINVAL = -1, EVAMX_ELAUNCH = -2, EVAMX_ENOSPACE = -3 };
+enum { EVAMX_DTYPE_F16 = 0, EVAMX_DTYPE_BF16 = 1 };
+enum { EVAMX_SCORE_SIGMOID = 0, EVAMX_SCORE_SQRT_SOFTPLUS = 1 };
+/* Device-side error flags (sticky bits in the workspace, read with evamx_moe_flags_ptr). */
+enum { EVAMX_ERR_EXPERT_RANGE = 1 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* evamx_last_error(void);
+/* ABI version of this library (incremented on incompatible changes). */
+int evamx_abi_version(void);
+
+/* ---- EXL3 decode ------------------------------------------------------------------------ */
+
+/* Decode one EXL3 projection to fp16 W[in][out] (row-major), bit-exact with the reference
+ * MUL1 codebook. trellis: device int16 [in/16][out/16][16*bits] (16b+8 at rate b+0.5).
+ * bits in {1..8} or {1.5, 2.5, 3.5}. */
+int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, float bits,
+                       void* w_fp16, evamx_stream_t stream);
+
+/* ---- single EXL3 linear (fp16 in, fp16 out) ---------------------------------------------- */
+
+size_t evamx_exl3_linear_workspace_bytes(int rows, int in_features, int out_features);
+
+/* y[rows][out] = svh * H(W^T H(x * suh)) with the reference's fp16 rounding points.
+ * rows in 1..16; in/out multiples of 128; bits in {2,3,4,5}. All pointers device. */
+int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, int out_features,
+                      const void* trellis, const void* suh_fp16, const void* svh_fp16, float bits,
+                      void* y_fp16, void* workspace, size_t workspace_bytes, evamx_stream_t stream);
+
+/* ---- router ------------------------------------------------------------------------------ */
+
+/* indices[r][j], weights[r][j] (fp32) and rw_fp16[r][j] = fp16(weights) for the top `topk`
+ * experts of each row of logits [rows][n_experts]: selection key score(z) + sel_bias (or z
+ * itself for sigmoid without a bias), ties to the lower index, slots ordered by descending
+ * key; weights = score / (sum + 1e-20) * route_scale. sel_bias: device [n_experts] or NULL. */
+int evamx_route_topk(const float* logits, const float* sel_bias, int rows, int n_experts, int topk,
+                     int score_fn, float route_scale, int64_t* indices, float* weights, void* rw_fp16,
+                     evamx_stream_t stream);
+
+/* ---- slot grouping (the reference's run table) ------------------------------------------- */
+
+size_t evamx_prepare_routes_workspace_bytes(int capacity, int topk);
+
+/* runs: device int32 [2 + 2*capacity*topk + 1] =
+ *   [n_runs, 0, run_start[0..capacity*topk], order[capacity*topk]] with unused entries zero:
+ * active slots (fp16 weight != 0) sorted by (expert, slot), cut at an expert change or every
+ * 8 slots. Expert indices outside [0, n_local) set EVAMX_ERR_EXPERT_RANGE in the workspace's
+ * flag word (evamx_prepare_routes_flags_ptr) and make the slot inactive. */
+int evamx_prepare_routes(const int64_t* sel, const void* rw_fp16, int rows, int topk, int capacity,
+                         int n_local, int32_t* runs, void* workspace, size_t workspace_bytes,
+                         evamx_stream_t stream);
+int32_t* evamx_prepare_routes_flags_ptr(void* workspace);
+
+/* ---- MoE layer forward --------------------------------------------------------------------- */
+
+typedef struct evamx_moe_shape {
+    int32_t rows_max;     /* token rows per call (capacity) */
+    int32_t hidden;       /* H, multiple of 128 */
+    int32_t inter;        /* I, multiple of 128 */
+    int32_t topk;         /* <= 32 */
+    int32_t n_local;      /* pointer-table entries, <= 512 */
+    int32_t has_shared;   /* 1: a shared expert is added to every row */
+    int32_t ksplit_gu;    /* k-splits of the gate/up GEMV (0: default for the shape) */
+    int32_t ksplit_down;  /* k-splits of the down GEMV (0: default for the shape) */
+} evamx_moe_shape;
+
+typedef struct evamx_moe_args {
+    evamx_moe_shape shape;
+    int32_t rows;                 /* T, 1..rows_max */
+    const void* x;                /* device [rows][x_stride] fp16 or bf16 */
+    int32_t x_dtype;              /* EVAMX_DTYPE_* */
+    int32_t x_stride;             /* elements; >= hidden */
+    /* routing: logits != NULL routes on device and writes sel/weights/rw_fp16; otherwise
+     * sel and weights (fp32) are inputs, or sel and rw_fp16 when weights == NULL */
+    const float* logits;          /* device [rows][n_logits] or NULL */
+    const float* sel_bias;        /* device [n_logits] or NULL */
+    int32_t n_logits;             /* experts in the logits (= n_local without expert ranges) */
+    int32_t score_fn;             /* EVAMX_SCORE_* */
+    float route_scale;
+    int64_t* sel;                 /* device [rows][topk] */
+    float* weights;               /* device [rows][topk] fp32, or NULL */
+    void* rw_fp16;                /* device [rows][topk] fp16, or NULL (workspace copy) */
+    int32_t min_expert;           /* -1: no expert range; else sel in [min, max) is local */
+    int32_t max_expert;
+    /* experts */
+    const int64_t* tables;        /* device int64 [9][n_local]: g_trellis, g_suh, g_svh,
+                                     u_trellis, u_suh, u_svh, d_trellis, d_suh, d_svh */
+    const uint8_t* k2_per_expert; /* device [n_local], 2*bits per expert, or NULL */
+    float bits;                   /* uniform rate when k2_per_expert is NULL: 2, 3, 4, 5 */
+    const int64_t* shared;        /* HOST array of 9 device pointers (table order) or NULL */
+    float shared_bits;
+    float limit;                  /* SwiGLU limit (0: none) */
+    /* output: out[r][0..hidden) = routed (slot order, fp32) + shared */
+    float* out;                   /* device */
+    int32_t out_stride;           /* elements; >= hidden */
+    void* workspace;              /* device, evamx_moe_workspace_bytes(&shape) bytes */
+    size_t workspace_bytes;
+} evamx_moe_args;
+
+size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape);
+/* Zero the workspace's sticky flag word (a kernel, not a memset: capture-safe). Call once
+ * after allocating the workspace. */
+int evamx_moe_workspace_init(const evamx_moe_shape* shape, void* workspace, evamx_stream_t stream);
+int evamx_moe_forward(const evamx_moe_args* args, evamx_stream_t stream);
+/* Device pointers into a workspace: the run table of the last forward (layout of
+ * evamx_prepare_routes with capacity = rows_max) and the sticky flag word. */
+int32_t* evamx_moe_runs_ptr(const evamx_moe_shape* shape, void* workspace);
+int32_t* evamx_moe_flags_ptr(const evamx_moe_shape* shape, void* workspace);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EVAMX_H */

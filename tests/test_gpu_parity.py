@@ -1,0 +1,199 @@
+"""GPU parity of the HIP kernels against the CPU oracle, on identical seeded inputs.
+
+Bars: decoded fp16 weights, router indices and run tables bit-exact; layer outputs within a
+max row-relative error of 1e-2 (max_r max|y_r - ref_r| / max|ref_r|).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import coop, exl3, synth
+from tests.gpu_helpers import DeviceExperts, rel_err_rows, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _ops():
+    from eva_amd import ops
+    return ops
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 1, 6, 8, 1.5, 2.5, 3.5])
+def test_dequant_bit_exact(dev, K):
+    ops = _ops()
+    rng = np.random.default_rng(int(K * 10))
+    n_in, n_out = 64, 256
+    tr = rng.integers(-32768, 32768, size=(n_in // 16, n_out // 16, exl3.tile_u16(K)), dtype=np.int16)
+    w = ops.exl3_dequant(to_dev(tr, dev), K).cpu().numpy()
+    ref = exl3.dequant(tr, K)
+    assert np.array_equal(w.view(np.uint16), ref.view(np.uint16))
+
+
+def test_dequant_dsv3_projection_bit_exact(dev):
+    ops = _ops()
+    rng = np.random.default_rng(7)
+    tr = rng.integers(-32768, 32768, size=(7168 // 16, 2048 // 16, 64), dtype=np.int16)
+    w = ops.exl3_dequant(to_dev(tr, dev), 4).cpu().numpy()
+    ref = coop.dequant_fast(tr, 4)
+    assert np.array_equal(w.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("score", ["sigmoid", "sqrt_softplus"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_route_topk_bit_exact(dev, score, bias):
+    ops = _ops()
+    rng = np.random.default_rng(3)
+    z = rng.standard_normal((37, 256)).astype(np.float32)
+    z[5] = 0.25                                       # all-equal row -> indices 0..k-1
+    z[6, 10:20] = 1.5                                 # ties inside the top-k
+    b = rng.standard_normal(256).astype(np.float32) * 0.1 if bias else None
+    idx, w, rw = ops.route_topk(to_dev(z, dev), 8, score, None if b is None else to_dev(b, dev), 2.5)
+    ridx, rwt = coop.route(z, 8, score, b, 2.5)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(w.cpu().numpy(), rwt)
+    assert np.array_equal(rw.cpu().numpy(), rwt.astype(np.float16))
+    if b is None:
+        assert np.array_equal(ridx[5], np.arange(8))
+
+
+@pytest.mark.parametrize("rows,topk,n_local,zero_frac", [(1, 8, 256, 0.0), (16, 8, 256, 0.1),
+                                                          (512, 6, 384, 0.05), (64, 8, 12, 0.0)])
+def test_prepare_routes_bit_exact(dev, rows, topk, n_local, zero_frac):
+    ops = _ops()
+    rng = np.random.default_rng(rows + topk)
+    sel = np.stack([rng.choice(n_local, size=topk, replace=False) for _ in range(rows)]).astype(np.int64)
+    rw = rng.uniform(0.05, 1.0, size=(rows, topk)).astype(np.float16)
+    rw[rng.uniform(size=rw.shape) < zero_frac] = 0
+    cap = rows + 3
+    runs = ops.prepare_routes(to_dev(sel, dev), to_dev(rw, dev), cap, n_local).cpu().numpy()
+    ref = coop.reference_table(sel, rw, capacity=cap)
+    assert np.array_equal(runs, ref)
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5])
+@pytest.mark.parametrize("rows", [1, 3, 16])
+def test_exl3_linear(dev, K, rows):
+    ops = _ops()
+    rng = np.random.default_rng(100 + rows)
+    tr, suh, svh = synth.projection(rng, 512, 384, K, svh_scale=1 / np.sqrt(512))
+    x = rng.standard_normal((rows, 512)).astype(np.float16)
+    y = ops.exl3_linear(to_dev(x, dev), to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), K).cpu().numpy()
+    ref = coop.exl3_linear(x, tr, suh, svh, K)
+    assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
+
+
+def _layer_case(rng, H, I, E, K, svh_scale, rates=None):
+    experts = []
+    for e in range(E):
+        k = K if rates is None else float(rates[e])
+        experts.append(synth.expert(rng, H, I, k, svh_scale))
+    shared = synth.expert(rng, H, I, K, svh_scale)
+    return experts, shared
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5, 16])
+@pytest.mark.parametrize("K", [2, 3, 4, 5])
+def test_moe_layer_small(dev, rows, K):
+    ops = _ops()
+    H, I, E, topk, limit = 512, 256, 24, 4, 10.0
+    rng = np.random.default_rng(1000 * rows + K)
+    experts, shared = _layer_case(rng, H, I, E, K, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, rows, H)
+    logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
+    ref, ridx, rw, rrw = coop.moe_layer(x, logits, experts, shared, topk, limit)
+
+    de = DeviceExperts(experts, dev)
+    ds = DeviceExperts([shared], dev)
+    ws = ops.MoeWorkspace(dev, rows_max=16, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    xt = to_dev(x, dev).to(torch.bfloat16)
+    sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, xt, de.table, out, limit=limit, bits=K, logits=to_dev(logits, dev), sel=sel, weights=w,
+                    shared_ptrs=ds.ptrs(0), shared_bits=K)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), ridx)
+    assert int(ws.flags().cpu()[0]) == 0
+    y = out.cpu().numpy()
+    assert rel_err_rows(y, ref) < TOL
+    runs = ws.runs().cpu().numpy()
+    assert np.array_equal(runs, coop.reference_table(ridx, rrw, capacity=16))
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_moe_layer_dsv3_shape(dev, rows):
+    """DeepSeek-V3 shape (H=7168, I=2048, 256 routed + 1 shared, top-8, 4 bpw), oracle on the
+    touched experts only."""
+    ops = _ops()
+    H, I, E, topk, limit, K = 7168, 2048, 256, 8, 10.0, 4
+    rng = np.random.default_rng(42 + rows)
+    x = synth.activations_bf16(rng, rows, H)
+    logits = synth.logits_plain(rng, rows, E) if rows == 1 else synth.logits_skewed(rng, rows, E)
+    ridx, rwt = coop.route(logits, topk)
+    used = sorted(set(int(v) for v in ridx.reshape(-1)))
+    experts = {e: synth.expert(rng, H, I, K, 1 / np.sqrt(H)) for e in used}
+    shared = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
+    ref, _, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+
+    # Device table: touched experts at their indices, a dummy expert everywhere else.
+    dummy = synth.expert(np.random.default_rng(0), H, I, K)
+    de = DeviceExperts([experts[e] for e in used] + [dummy], dev)
+    table = torch.empty(9, E, dtype=torch.int64)
+    cols = {e: i for i, e in enumerate(used)}
+    host = de.table.cpu()
+    for e in range(E):
+        table[:, e] = host[:, cols.get(e, len(used))]
+    table = table.to(dev)
+    ds = DeviceExperts([shared], dev)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), table, out, limit=limit, bits=K,
+                    logits=to_dev(logits, dev), sel=sel, weights=w, shared_ptrs=ds.ptrs(0), shared_bits=K)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), ridx)
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+
+
+def test_moe_mixed_rates_and_given_routes(dev):
+    ops = _ops()
+    H, I, E, topk, limit = 256, 256, 10, 3, 0.0
+    rng = np.random.default_rng(5)
+    rates = synth.mixed_rates(rng, E)
+    experts, _ = _layer_case(rng, H, I, E, 4, 1 / np.sqrt(H), rates)
+    rows = 7
+    x = rng.standard_normal((rows, H)).astype(np.float16)
+    sel = np.stack([rng.choice(E, size=topk, replace=False) for _ in range(rows)]).astype(np.int64)
+    rw = rng.uniform(0.1, 1.0, size=(rows, topk)).astype(np.float16)
+    rw[2, 1] = 0                                                  # one inactive slot
+    ref = coop.moe_routed(x, sel, rw, experts, limit)
+    de = DeviceExperts(experts, dev)
+    ws = ops.MoeWorkspace(dev, rows_max=8, hidden=H, inter=I, topk=topk, n_local=E, has_shared=False)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev), de.table, out, limit=limit, k2_per_expert=de.k2,
+                    sel=to_dev(sel, dev), rw=to_dev(rw, dev))
+    torch.cuda.synchronize()
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+
+
+def test_moe_out_of_range_expert_sets_flag(dev):
+    ops = _ops()
+    H, I, E, topk = 256, 128, 8, 2
+    rng = np.random.default_rng(9)
+    experts, _ = _layer_case(rng, H, I, E, 4, 1 / np.sqrt(H))
+    de = DeviceExperts(experts, dev)
+    ws = ops.MoeWorkspace(dev, rows_max=2, hidden=H, inter=I, topk=topk, n_local=E, has_shared=False)
+    x = rng.standard_normal((2, H)).astype(np.float16)
+    sel = np.array([[1, 99], [2, 3]], dtype=np.int64)              # 99 is outside the table
+    rw = np.array([[0.5, 0.5], [0.5, 0.5]], dtype=np.float16)
+    out = torch.empty(2, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev), de.table, out, limit=0.0, bits=4, sel=to_dev(sel, dev), rw=to_dev(rw, dev))
+    torch.cuda.synchronize()
+    assert int(ws.flags().cpu()[0]) & 1
+    rw2 = rw.copy()
+    rw2[0, 1] = 0                                                  # the flagged slot is dropped
+    ref = coop.moe_routed(x, np.where(sel < E, sel, 0), rw2, experts, 0.0)
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
