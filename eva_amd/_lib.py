@@ -36,7 +36,8 @@ class MoeArgs(ctypes.Structure):
                 ("route_scale", _f32), ("sel", _vp), ("weights", _vp), ("rw_fp16", _vp),
                 ("min_expert", _i32), ("max_expert", _i32), ("tables", _vp), ("k2_per_expert", _vp),
                 ("bits", _f32), ("shared", _vp), ("shared_bits", _f32), ("limit", _f32),
-                ("out", _vp), ("out_stride", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t)]
+                ("out", _vp), ("out_stride", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+                ("events", _vp)]
 
 
 class EvamxError(RuntimeError):

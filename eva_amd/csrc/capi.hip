@@ -40,7 +40,7 @@ static bool gemv_rate(int k2) { return k2 == 4 || k2 == 6 || k2 == 8 || k2 == 10
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t flags, meta, local, order, runs, chunks, tok_cnt, ctr_gu, ctr_d, rw16, xr, act, part_gu, part_d, total;
+    size_t flags, meta, local, order, runs, chunks, rw16, xr, xsum, act, actsum, part_gu, part_d, total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d;
 };
 
@@ -49,6 +49,20 @@ static int default_ksplit(int work_items, int kt_n, int target)
     int ks = (target + work_items - 1) / work_items;
     const int cap = kt_n / 8 < 16 ? kt_n / 8 : 16;
     if (ks > cap) ks = cap;
+    if (ks < 1) ks = 1;
+    return ks;
+}
+
+// Down-GEMV k-splits cover whole 128-element chunks of I.
+static int down_ksplit(int requested, int work_items, int inter)
+{
+    const int na = inter / 128;
+    int ks = requested;
+    if (ks <= 0) {
+        ks = (4096 + work_items - 1) / work_items;
+        if (ks > 16) ks = 16;
+    }
+    if (ks > na) ks = na;
     if (ks < 1) ks = 1;
     return ks;
 }
@@ -82,8 +96,9 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     const int routed_chunks = (L.slots_max < s->n_local ? L.slots_max : s->n_local) + L.slots_max / EVAMX_CHUNK;
     L.max_chunks = routed_chunks + (s->has_shared ? (s->rows_max + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
     const int chunks_est = (L.slots_max < s->n_local ? L.slots_max : s->n_local) + (s->has_shared ? 1 : 0);
-    L.ks_gu = s->ksplit_gu ? s->ksplit_gu : default_ksplit(chunks_est * 2 * (s->inter / 128), s->hidden / 16, 2048);
-    L.ks_d = s->ksplit_down ? s->ksplit_down : default_ksplit(chunks_est * (s->hidden / 128), s->inter / 16, 2048);
+    L.ks_gu = s->ksplit_gu ? s->ksplit_gu : default_ksplit(chunks_est * 2 * (s->inter / 128), s->hidden / 16, 4096);
+    if (L.ks_gu > s->hidden / 128) L.ks_gu = s->hidden / 128;
+    L.ks_d = down_ksplit(s->ksplit_down, chunks_est * (s->hidden / 128), s->inter);
     size_t o = 0;
     L.flags = o;   o = al256(o + 64 * 4);
     L.meta = o;    o = al256(o + 64 * 4);
@@ -91,12 +106,11 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.order = o;   o = al256(o + (size_t)L.nslot_max * 4);
     L.runs = o;    o = al256(o + (size_t)(2 + 2 * L.slots_max + 1) * 4);
     L.chunks = o;  o = al256(o + (size_t)L.max_chunks * 16);
-    L.tok_cnt = o; o = al256(o + (size_t)s->rows_max * 4);
-    L.ctr_gu = o;  o = al256(o + (size_t)L.max_chunks * (s->inter / 128) * 4);
-    L.ctr_d = o;   o = al256(o + (size_t)s->rows_max * (s->hidden / 128) * 4);
     L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
     L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
+    L.xsum = o;    o = al256(o + (size_t)2 * L.nslot_max * (s->hidden / 128) * 4);
     L.act = o;     o = al256(o + (size_t)L.nslot_max * s->inter * 2);
+    L.actsum = o;  o = al256(o + (size_t)L.nslot_max * (s->inter / 128) * 4);
     L.part_gu = o; o = al256(o + (size_t)L.ks_gu * 2 * L.nslot_max * s->inter * 4);
     L.part_d = o;  o = al256(o + (size_t)L.ks_d * L.nslot_max * s->hidden * 4);
     L.total = o;
@@ -334,16 +348,15 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.slots_max = L.slots_max;
     p.chunks = (int*)(ws + L.chunks);
     p.max_chunks = L.max_chunks;
-    p.tok_cnt = (int*)(ws + L.tok_cnt);
-    p.ctr_gu = (int*)(ws + L.ctr_gu); p.ctr_gu_len = L.max_chunks * (s->inter / 128);
-    p.ctr_d = (int*)(ws + L.ctr_d); p.ctr_d_len = s->rows_max * (s->hidden / 128);
     p.xr = (half_t*)(ws + L.xr);
+    p.xsum = (float*)(ws + L.xsum);
     p.act = (half_t*)(ws + L.act);
+    p.actsum = (float*)(ws + L.actsum);
     p.part_gu = (float*)(ws + L.part_gu);
     p.part_d = (float*)(ws + L.part_d);
     p.nslot_max = L.nslot_max;
     p.ks_gu = L.ks_gu; p.ks_d = L.ks_d;
     p.out = a->out; p.out_stride = a->out_stride;
-    moe_launch(p, (hipStream_t)stream);
+    moe_launch(p, (hipStream_t)stream, a->events);
     return launched("moe_forward");
 }

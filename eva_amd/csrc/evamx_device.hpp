@@ -56,6 +56,19 @@ __device__ __forceinline__ half2_t mul1_pair(uint32_t p0, uint32_t p1)
     return __builtin_elementwise_fma(h, k, b);
 }
 
+// The fp16 pair (1024 + bytesum) of two hashes, before the codebook's affine map: the decode
+// GEMV multiplies these by the activations and applies w = 0x1eee * h + 0xc931 once per column
+// (sum_k x_k w_k = 0x1eee * sum_k x_k h_k + 0xc931 * sum_k x_k).
+__device__ __forceinline__ half2_t mul1_hpair(uint32_t p0, uint32_t p1)
+{
+    uint32_t s = __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u);
+    s = __builtin_amdgcn_sad_hi_u8(p1, 0u, s);
+    return __builtin_bit_cast(half2_t, s);
+}
+
+constexpr float MUL1_K_INV = 0.00676727294921875f;   // fp16 0x1eee
+constexpr float MUL1_K_BIAS = -10.3828125f;          // fp16 0xc931
+
 __device__ __forceinline__ half_t mul1_one(uint32_t state)
 {
     const half2_t w = mul1_pair(mul1_hash<false>(state), 0u);
@@ -96,18 +109,23 @@ __device__ __forceinline__ uint32_t win_reg(const LaneWords<K>& w)
     return funnel(w.b[L - 1], w.b[L], S);
 }
 
-// Hash of lane-local position j (0..31). When the window 16 bits later is also in range
-// (K divides 16), the window sits in the high half of that window's register, so pairs
-// share one funnel shift.
+// Hash of lane-local position j (0..31). When K divides 16, the windows of positions j and
+// j + 16/K are 16 bits apart and share one funnel shift: with P = 16/K, positions in odd
+// P-blocks take the low half of their own register, positions in even P-blocks the high half
+// of the register of j + P.
 template <int K, int J>
 __device__ __forceinline__ uint32_t lane_hash(const LaneWords<K>& w)
 {
     constexpr int E = win_end<K>(J);
-    constexpr bool SHARE = (16 % K == 0) && (J + 16 / K) < 32;
-    if constexpr (SHARE)
-        return mul1_hash<true>(win_reg<K, E + 16>(w));
-    else
+    if constexpr (16 % K == 0) {
+        constexpr int P = 16 / K;
+        if constexpr ((J / P) % 2 == 0)
+            return mul1_hash<true>(win_reg<K, E + 16>(w));
+        else
+            return mul1_hash<false>(win_reg<K, E>(w));
+    } else {
         return mul1_hash<false>(win_reg<K, E>(w));
+    }
 }
 
 // Decoded weight pair of lane-local positions (J, J+1) (J even): same column, k and k+1.
@@ -117,18 +135,47 @@ __device__ __forceinline__ half2_t lane_pair(const LaneWords<K>& w)
     return mul1_pair(lane_hash<K, J>(w), lane_hash<K, J + 1>(w));
 }
 
+// The (1024 + bytesum) pair of the same positions (see mul1_hpair).
+template <int K, int J>
+__device__ __forceinline__ half2_t lane_hpair(const LaneWords<K>& w)
+{
+    return mul1_hpair(lane_hash<K, J>(w), lane_hash<K, J + 1>(w));
+}
+
 // ---------------------------------------------------------------------------------------------
 // Wave-level 128-point Hadamard in the reference's fp32 evaluation order: radix-2 on element
 // bits 0..6 in increasing order, lower index a+b, upper a-b, scale last. Bit-identical to the
 // reference for any data layout, because IEEE addition is commutative and each stage's
 // operand pairs are the same.
 
-// Butterfly where the partner lives in another lane (lane ^ m); `upper` = this lane holds the
-// element with the stage bit set.
-__device__ __forceinline__ float bfly_x(float v, int m, bool upper)
+// Value of lane (lane ^ M) for a compile-time M: DPP for M < 16 (quad permutes, row
+// rotations), an LDS-unit swizzle for 16 and a bpermute for 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane)
 {
-    const float p = __shfl_xor(v, m, WAVE);
-    return upper ? (p - v) : (v + p);
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, false); // quad_perm [2,3,0,1]
+    else if constexpr (M == 4) {
+        const uint32_t r4 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xf, 0xf, false);       // row_ror:4
+        const uint32_t r12 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x12C, 0xf, 0xf, false);      // row_ror:12
+        return (lane & 4) ? r4 : r12;
+    } else if constexpr (M == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false); // row_ror:8
+    else if constexpr (M == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);           // xor 16 in 32
+    else return (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ M) << 2, (int)v);
+}
+
+template <int M>
+__device__ __forceinline__ float xor_lane_f(float v, int lane)
+{
+    return __builtin_bit_cast(float, xor_lane<M>(__builtin_bit_cast(uint32_t, v), lane));
+}
+
+// Butterfly where the partner lives in lane ^ M; the upper lane (stage bit set) takes a - b.
+template <int M>
+__device__ __forceinline__ float bfly_x(float v, int lane)
+{
+    const float p = xor_lane_f<M>(v, lane);
+    return (lane & M) ? (p - v) : (v + p);
 }
 
 }  // namespace evamx

@@ -23,25 +23,17 @@ __device__ __forceinline__ int lane_col(int lane, int h) { return 16 * (lane >> 
 
 __device__ __forceinline__ void had128_lane(float& v0, float& v1, int lane)
 {
-#pragma unroll
-    for (int b = 0; b < 3; ++b) {
-        const int m = 1 << b;
-        const bool up = (lane & m) != 0;
-        v0 = bfly_x(v0, m, up);
-        v1 = bfly_x(v1, m, up);
-    }
+    v0 = bfly_x<1>(v0, lane);  v1 = bfly_x<1>(v1, lane);
+    v0 = bfly_x<2>(v0, lane);  v1 = bfly_x<2>(v1, lane);
+    v0 = bfly_x<4>(v0, lane);  v1 = bfly_x<4>(v1, lane);
     {
         const float a = v0, c = v1;
         v0 = a + c;
         v1 = a - c;
     }
-#pragma unroll
-    for (int b = 3; b < 6; ++b) {
-        const int m = 1 << b;
-        const bool up = (lane & m) != 0;
-        v0 = bfly_x(v0, m, up);
-        v1 = bfly_x(v1, m, up);
-    }
+    v0 = bfly_x<8>(v0, lane);  v1 = bfly_x<8>(v1, lane);
+    v0 = bfly_x<16>(v0, lane); v1 = bfly_x<16>(v1, lane);
+    v0 = bfly_x<32>(v0, lane); v1 = bfly_x<32>(v1, lane);
     v0 *= R_SCALE;
     v1 *= R_SCALE;
 }
@@ -72,59 +64,77 @@ __device__ __forceinline__ void load_words(LaneWords<K>& w, const uint32_t* p)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Decode GEMV over one wave's k-range: acc[m][h] += sum_k A[slot_m][k] * W[k][col(lane,h)] for
-// the tm (<= TM) rows slot_of[0..tm) of A (fp16, row stride a_stride elements).
+// Activation rows of a GEMV chunk: row m holds the k-vector of slot slot_of[m], read through
+// wave-uniform addresses (scalar loads), together with its per-128-chunk sums (fp32) that the
+// affine codebook map needs.
+
+struct GlobalRows {
+    const half_t* A;
+    size_t stride;          // elements per row
+    const float* sums;      // [row][chunk] sums of the fp16 row values over 128-element chunks
+    int sums_stride;        // chunks per row
+};
+
+// ---------------------------------------------------------------------------------------------
+// Decode GEMV over one wave's k-range [16*kt0, 16*kt1): acc[m][h] = sum_k X[m][k] * h_k,
+// h_k = 1024 + bytesum of the weight at (k, col(lane, h)) (see mul1_hpair).
+
+// The previous word of a lane's tile run: lane (l & ~7) | ((l - 1) & 7)'s last word. DPP row
+// rotations within rows of 16 lanes: rotate by 1 serves lanes with l % 8 != 0, rotate by 9 the
+// first lane of each group of 8 (no LDS round trip, unlike a bpermute).
+__device__ __forceinline__ uint32_t prev_word(uint32_t v, int lane)
+{
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xf, 0xf, false);   // row_ror:1
+    const uint32_t r9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x129, 0xf, 0xf, false);   // row_ror:9
+    return (lane & 7) ? r1 : r9;
+}
+
+// Weight prefetch depth (k-slices in flight per wave): deeper for narrow chunks, whose loop
+// body is short; wide chunks keep register pressure in check.
+template <int TM>
+constexpr int prefetch_depth() { return TM <= 2 ? 8 : 4; }
 
 template <int K, int TM>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
-                                          const half_t* __restrict__ A, size_t a_stride, const int* slot_of,
-                                          int tm, float (&acc)[TM][2])
+                                          const GlobalRows& src, const uint32_t (&aoff)[TM], int tm, float (&acc)[TM][2])
 {
     constexpr int TW = 8 * K;
-    constexpr int PF = 4;
+    constexpr int PF = prefetch_depth<TM>();
     const int lane = threadIdx.x & 63;
     const int q = lane & 7;
-    const int src = (lane & ~7) | ((q + 7) & 7);
     const size_t slice = (size_t)nt_n * TW;
     const uint32_t* bp = trellis + (size_t)(cg * 8 + (lane >> 3)) * TW + q * K;
 
 #pragma unroll
     for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = 0.0f;
 
-    // Row offsets of the activation rows (wave-uniform: the loads below become scalar loads)
-    uint32_t aoff[TM];
-#pragma unroll
-    for (int m = 0; m < TM; ++m)
-        aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tm ? slot_of[m] : slot_of[0]) * (int)(a_stride / 8));
-
+    // Prefetch ring: the row PF slices ahead, clamped to the wave's last row so that the steady
+    // state needs no branch and never reads outside the matrix (the clamped reloads hit cache).
     LaneWords<K> ring[PF];
+    const int last = kt1 - 1;
 #pragma unroll
-    for (int d = 0; d < PF; ++d)
-        if (kt0 + d < kt1) load_words<K>(ring[d], bp + (size_t)(kt0 + d) * slice);
+    for (int d = 0; d < PF; ++d) load_words<K>(ring[d], bp + (size_t)min(kt0 + d, last) * slice);
 
-    for (int kb = kt0; kb < kt1; kb += PF) {
-#pragma unroll
-        for (int d = 0; d < PF; ++d) {
-            const int kt = kb + d;
-            if (kt < kt1) {
-            LaneWords<K> w = ring[d];
-            if (kt + PF < kt1) load_words<K>(ring[d], bp + (size_t)(kt + PF) * slice);
-            w.b[0] = __shfl(w.b[K], src, WAVE);
-            half2_t wp[16];
+    auto step = [&](int kt, LaneWords<K>& slot) {
+        LaneWords<K> w = slot;
+        const int pre = __builtin_amdgcn_readfirstlane(min(kt + PF, last));
+        load_words<K>(slot, bp + (size_t)pre * slice);
+        w.b[0] = prev_word(w.b[K], lane);
+        half2_t wp[16];
 #define EVAMX_DEC_UNIT(U)                                \
-            wp[4 * U + 0] = lane_pair<K, 8 * U + 0>(w);  \
-            wp[4 * U + 1] = lane_pair<K, 8 * U + 2>(w);  \
-            wp[4 * U + 2] = lane_pair<K, 8 * U + 4>(w);  \
-            wp[4 * U + 3] = lane_pair<K, 8 * U + 6>(w);
-            EVAMX_DEC_UNIT(0)
-            EVAMX_DEC_UNIT(1)
-            EVAMX_DEC_UNIT(2)
-            EVAMX_DEC_UNIT(3)
+        wp[4 * U + 0] = lane_hpair<K, 8 * U + 0>(w);     \
+        wp[4 * U + 1] = lane_hpair<K, 8 * U + 2>(w);     \
+        wp[4 * U + 2] = lane_hpair<K, 8 * U + 4>(w);     \
+        wp[4 * U + 3] = lane_hpair<K, 8 * U + 6>(w);
+        EVAMX_DEC_UNIT(0)
+        EVAMX_DEC_UNIT(1)
+        EVAMX_DEC_UNIT(2)
+        EVAMX_DEC_UNIT(3)
 #undef EVAMX_DEC_UNIT
 #pragma unroll
-            for (int m = 0; m < TM; ++m) {
-                if (m < tm) {
-                const half2_t* xp = (const half2_t*)A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
+        for (int m = 0; m < TM; ++m) {
+            if (m < tm) {
+                const half2_t* xp = (const half2_t*)src.A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
                 half2_t xa[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) xa[i] = xp[i];
@@ -138,33 +148,51 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
                 }
                 acc[m][0] = a0;
                 acc[m][1] = a1;
-                }
-            }
             }
         }
+        // keep the next step's scalar activation loads out of this one (register pressure)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    int kt = kt0;
+    for (; kt + PF <= kt1; kt += PF) {
+#pragma unroll
+        for (int d = 0; d < PF; ++d) step(kt + d, ring[d]);
     }
+#pragma unroll
+    for (int d = 0; d < PF - 1; ++d)
+        if (kt + d < kt1) step(kt + d, ring[d]);
 }
 
-// GEMV for a chunk of tm rows with the smallest template that fits; writes fp32 partials
-// part[slot_of[m] * part_stride + column].
+// GEMV for a chunk of tm rows over the 128-element k-chunks [c0, c1) with the smallest
+// template that fits; writes fp32 partials part[slot_of[m] * part_stride + column] =
+// sum_k x_k w_k = 0x1eee * sum_k x_k h_k + 0xc931 * sum_k x_k.
 template <int K>
-__device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, int cg, int kt0, int kt1,
-                                           const half_t* A, size_t a_stride, const int* slot_of, int tm,
-                                           float* part, size_t part_stride)
+__device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
+                                           const GlobalRows& src, const int* slot_of, int tm, float* part,
+                                           size_t part_stride)
 {
     const int lane = threadIdx.x & 63;
-    const int c0 = cg * 128 + lane_col(lane, 0), c1 = cg * 128 + lane_col(lane, 1);
-#define EVAMX_RUN(TMV)                                                                        \
-    {                                                                                         \
-        float acc[TMV][2];                                                                    \
-        gemv_wave<K, TMV>(trellis, nt_n, cg, kt0, kt1, A, a_stride, slot_of, tm, acc);        \
-        _Pragma("unroll") for (int m = 0; m < TMV; ++m) {                                     \
-            if (m < tm) {                                                                     \
-                float* dst = part + (size_t)slot_of[m] * part_stride;                         \
-                dst[c0] = acc[m][0];                                                          \
-                dst[c1] = acc[m][1];                                                          \
-            }                                                                                 \
-        }                                                                                     \
+    const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
+#define EVAMX_RUN(TMV)                                                                          \
+    {                                                                                           \
+        uint32_t aoff[TMV];                                                                     \
+        _Pragma("unroll") for (int m = 0; m < TMV; ++m)                                         \
+            aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tm ? slot_of[m] : slot_of[0]) * \
+                                                               (int)(src.stride / 8));          \
+        float acc[TMV][2];                                                                      \
+        gemv_wave<K, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, src, aoff, tm, acc);               \
+        _Pragma("unroll") for (int m = 0; m < TMV; ++m) {                                       \
+            if (m < tm) {                                                                       \
+                const int row = slot_of[m];                                                     \
+                const float* sp = src.sums + (size_t)row * src.sums_stride;                     \
+                float xs = 0.0f;                                                                \
+                for (int c = c0; c < c1; ++c) xs += sp[c];                                      \
+                float* dst = part + (size_t)row * part_stride;                                  \
+                dst[col0] = MUL1_K_INV * acc[m][0] + MUL1_K_BIAS * xs;                          \
+                dst[col1] = MUL1_K_INV * acc[m][1] + MUL1_K_BIAS * xs;                          \
+            }                                                                                   \
+        }                                                                                       \
     }
     if (tm <= 1) EVAMX_RUN(1)
     else if (tm <= 2) EVAMX_RUN(2)
@@ -175,33 +203,30 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
 }
 
 // Runtime rate (k2 = 2K) -> instantiated GEMV; integer rates 2..5.
-__device__ __forceinline__ void gemv_dispatch_k(int k2, const uint32_t* trellis, int nt_n, int cg, int kt0, int kt1,
-                                                const half_t* A, size_t a_stride, const int* slot_of, int tm,
-                                                float* part, size_t part_stride)
+__device__ __forceinline__ void gemv_dispatch_k(int k2, const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
+                                                const GlobalRows& src, const int* slot_of, int tm, float* part,
+                                                size_t part_stride)
 {
     switch (k2) {
-        case 4: gemv_chunk<2>(trellis, nt_n, cg, kt0, kt1, A, a_stride, slot_of, tm, part, part_stride); break;
-        case 6: gemv_chunk<3>(trellis, nt_n, cg, kt0, kt1, A, a_stride, slot_of, tm, part, part_stride); break;
-        case 8: gemv_chunk<4>(trellis, nt_n, cg, kt0, kt1, A, a_stride, slot_of, tm, part, part_stride); break;
-        case 10: gemv_chunk<5>(trellis, nt_n, cg, kt0, kt1, A, a_stride, slot_of, tm, part, part_stride); break;
+        case 4: gemv_chunk<2>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 6: gemv_chunk<3>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 8: gemv_chunk<4>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 10: gemv_chunk<5>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
         default: break;
     }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Completion counter (exl3_moe_coop_kernel.cuh:549-559 semantics, per wave): every lane's stores
-// are released at device scope, one lane arrives; true (wave-uniform) for the last of `expected`
-// arrivals, which then acquires and may read the other waves' results.
-
-__device__ __forceinline__ bool arrive_last(int* ctr, int expected)
+// Sum over the wave of one value per lane (order fixed by the butterfly).
+__device__ __forceinline__ float wave_sum(float v)
 {
-    __threadfence();
-    int old = 0;
-    if ((threadIdx.x & 63) == 0) old = atomicAdd(ctr, 1);
-    old = __shfl(old, 0, WAVE);
-    const bool last = old == expected - 1;
-    if (last) __threadfence();
-    return last;
+    const int lane = threadIdx.x & 63;
+    v += xor_lane_f<1>(v, lane);
+    v += xor_lane_f<2>(v, lane);
+    v += xor_lane_f<4>(v, lane);
+    v += xor_lane_f<8>(v, lane);
+    v += xor_lane_f<16>(v, lane);
+    v += xor_lane_f<32>(v, lane);
+    return v;
 }
 
 }  // namespace evamx

@@ -13,7 +13,7 @@ int launch_dequant(const void* trellis, int in, int out, int k2, void* w, bool s
 
 namespace evamx {
 
-size_t linear_workspace(int rows, int in, int out, size_t* off_part, size_t* off_ctr);
+size_t linear_workspace(int rows, int in, int out, size_t* off_part, size_t* off_sum);
 int launch_linear(const void* x, int rows, int in, int out, const void* trellis, const void* suh,
                   const void* svh, int k2, void* y, void* ws, hipStream_t stream);
 

@@ -52,11 +52,10 @@ struct MoeParams {
     int* chunks;               // [max_chunks][4]: expert (-1 shared), begin, count, k2
     int max_chunks;
     int* meta;                 // [0] n_chunks, [1] n_active
-    int* ctr_gu; int ctr_gu_len;
-    int* ctr_d; int ctr_d_len;
-    int* tok_cnt;              // [T]
-    half_t* xr;                // [2][nslot_max][H]
-    half_t* act;               // [nslot_max][I]
+    half_t* xr;                // [2][nslot_max][H] rotated gate/up inputs
+    float* xsum;               // [2][nslot_max][H/128] their 128-chunk sums
+    half_t* act;               // [nslot_max][I] rotated down inputs
+    float* actsum;             // [nslot_max][I/128]
     float* part_gu;            // [ks_gu][2][nslot_max][I]
     float* part_d;             // [ks_d][nslot_max][H]
     int nslot_max;
@@ -66,7 +65,8 @@ struct MoeParams {
     int out_stride;
 };
 
-int moe_launch(MoeParams& p, hipStream_t stream);
+int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);
 int moe_prepare_only(MoeParams& p, hipStream_t stream);
+bool moe_small_path(int T, int topk);
 
 }  // namespace evamx

@@ -1,22 +1,26 @@
 // Decode-shaped cooperative EXL3 MoE layer on gfx950.
 //
 // Replaces the reference's prepare/rot/A/B launch sequence
-// (runtime/ds41/csrc/moe_coop3072/moe_coop3072.cu:42-71) with four launches on one stream, no
-// host synchronisation and no host-side memset (graph-capturable):
+// (runtime/ds41/csrc/moe_coop3072/moe_coop3072.cu:42-71). Cross-workgroup results only ever
+// cross a kernel boundary: a device-scope release fence costs an L2 write-back on this
+// multi-XCD part, far more than a launch when thousands of waves would each need one. Five
+// launches on one stream, no host synchronisation, no memset (graph-capturable):
 //
-//   moe_prepare   (1 block)  routing (optional), slot activity + bounds flag, the reference
-//                            run table (runs <= 8 slots, prepare_runs.cuh:8-66), per-expert
-//                            chunks of <= 16 slots, counter reset
-//   moe_rotate               per (slot, 128-chunk, gate|up): fp16(H128(x * suh))
-//                            (exl3_moe_coop_kernel.cuh:613-629; shared expert: fp16 pre-scale,
-//                            hadamard_inner.cuh:109-115)
-//   moe_gemv_gu              per (chunk, gate|up, 128 columns, k-split): decode-GEMV; the last
-//                            arrival per (chunk, 128 columns) runs the activation epilogue
-//                            (exl3_moe_coop_kernel.cuh:758-806; shared: model.py:450-452)
-//   moe_gemv_down            per (chunk, 128 columns, k-split): decode-GEMV; the last arrival
-//                            per (token, 128 columns) reduces the token's slots in slot order
-//                            and adds the shared expert (exl3_moe_coop_kernel.cuh:860-962,
-//                            model.py:498)
+//   moe_prepare   routing (optional), slot activity + bounds flag, stable grouping by expert
+//                 (the reference run table, runs <= 8 slots: prepare_runs.cuh:8-66; and chunks
+//                 of <= 16 slots for the GEMV work items), then the input rotation
+//                 fp16(H128(x * suh)) of every active slot (exl3_moe_coop_kernel.cuh:613-629;
+//                 shared expert: fp16 pre-scale, hadamard_inner.cuh:109-115). For <= 16 rows
+//                 every workgroup groups redundantly in LDS and rotates its share; workgroup 0
+//                 publishes the tables.
+//   moe_gate_up   per (chunk, gate|up, 128 columns, k-split) wave: decode GEMV -> fp32 partials
+//   moe_act       per (active slot, 128 columns of I): sums the gate/up partials in fixed
+//                 order, rounds to fp16 (gu_f32 = false), and runs the activation epilogue
+//                 (exl3_moe_coop_kernel.cuh:758-806; shared expert: model.py:450-452)
+//   moe_down      per (chunk, 128 columns, k-split) wave: decode GEMV -> fp32 partials
+//   moe_combine   per (token, 128 columns): output rotation * svh * routing weight, summed over
+//                 the token's slots in slot order, plus the shared expert
+//                 (exl3_moe_coop_kernel.cuh:860-962, model.py:498)
 #include "evamx_gemv.hpp"
 #include "evamx_internal.hpp"
 #include "evamx_moe.hpp"
@@ -66,6 +70,12 @@ __device__ float score_fn(float z, int fn)
     const float sp = fmaxf(z, 0.0f) + log1p_portable(exp_portable(-fabsf(z)));
     return sqrtf(sp);
 }
+
+__device__ float route_weight(float s, float tot, float scale)
+{
+    const float w = s / (tot + 1e-20f);
+    return w * scale;
+}
 #pragma clang fp contract(on)
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
@@ -78,111 +88,140 @@ __device__ __forceinline__ half_t load_x16(const void* x, int dtype, size_t i)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Prepare: one block of 1024 threads.
+// Routing of one token by one wave: top-k by (key desc, index asc); weights from the scores.
+// Lane j < topk writes slot j to sel_o / rw_o and, when publishing, to the global outputs.
+// Keys are packed as (order-preserving key bits << 32 | ~index) so that one 64-bit max, reduced
+// with lane butterflies, yields the winner and the tie rule at once (+0 and -0 compare equal).
 
-struct PrepShared {
-    int cnt[EVAMX_MAX_EXPERTS];
+__device__ __forceinline__ uint64_t pack_key(float k, int e)
+{
+    if (k == 0.0f) k = 0.0f;
+    const uint32_t u = __builtin_bit_cast(uint32_t, k);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+
+template <int M>
+__device__ __forceinline__ uint64_t max_x(uint64_t v, int lane)
+{
+    const uint32_t lo = xor_lane<M>((uint32_t)v, lane);
+    const uint32_t hi = xor_lane<M>((uint32_t)(v >> 32), lane);
+    const uint64_t p = ((uint64_t)hi << 32) | lo;
+    return p > v ? p : v;
+}
+
+__device__ void route_token(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
+{
+    constexpr int NPER = EVAMX_MAX_EXPERTS / 64;
+    const float* z = p.logits + (size_t)r * p.n_logits;
+    float zr[NPER];
+    uint64_t key[NPER];
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = lane + 64 * i;
+        zr[i] = e < p.n_logits ? z[e] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = lane + 64 * i;
+        float k = -INFINITY;
+        if (e < p.n_logits) {
+            const float zz = zr[i];
+            if (p.sel_bias) k = score_fn(zz, p.score) + p.sel_bias[e];
+            else k = (p.score == EVAMX_SCORE_SIGMOID) ? zz : score_fn(zz, p.score);
+        }
+        key[i] = e < p.n_logits ? pack_key(k, e) : 0ull;
+    }
+    float tot = 0.0f, my_score = 0.0f;
+    int my_id = 0;
+    for (int j = 0; j < p.topk; ++j) {
+        uint64_t best = 0ull;
+#pragma unroll
+        for (int i = 0; i < NPER; ++i) best = key[i] > best ? key[i] : best;
+        best = max_x<1>(best, lane);
+        best = max_x<2>(best, lane);
+        best = max_x<4>(best, lane);
+        best = max_x<8>(best, lane);
+        best = max_x<16>(best, lane);
+        best = max_x<32>(best, lane);
+        const int bi = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)best));
+        float mine = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPER; ++i) {
+            if (lane + 64 * i == bi) {
+                key[i] = 0ull;
+                mine = zr[i];
+            }
+        }
+        const float sc = score_fn(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), bi & 63)),
+                                  p.score);
+        tot = tot + sc;
+        if (lane == j) { my_score = sc; my_id = bi; }
+    }
+    if (lane < p.topk) {
+        const float w = route_weight(my_score, tot, p.route_scale);
+        const int s = r * p.topk + lane;
+        if (sel_o) sel_o[s] = my_id;
+        if (rw_o) rw_o[s] = f2h(w);
+        if (publish) {
+            p.sel[s] = my_id;
+            p.weights[s] = w;
+            p.rw16[s] = f2h(w);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Grouping by one workgroup. Per-slot arrays (local, order) may live in LDS or global memory;
+// per-expert arrays live in LDS.
+
+struct ExpertLds {
+    int cnt[EVAMX_MAX_EXPERTS + 1];
     int off[EVAMX_MAX_EXPERTS + 1];
     int run_base[EVAMX_MAX_EXPERTS + 1];
     int chunk_base[EVAMX_MAX_EXPERTS + 1];
-    int n_active;
+    int fill[EVAMX_MAX_EXPERTS];
 };
 
-__device__ void block_exclusive_scan(int* a, int n)
+// Exclusive scan of a[0..n) in place by one wave, a[n] = total (n <= 1024).
+__device__ void wave_excl_scan(int* a, int n, int lane)
 {
-    // In place exclusive scan of a[0..n) (n <= 1024) with a[n] = total; 1024 threads.
-    const int t = threadIdx.x;
-    __shared__ int buf[2][1024];
-    int v = (t < n) ? a[t] : 0;
-    buf[0][t] = v;
-    __syncthreads();
-    int src = 0;
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int x = buf[src][t] + ((t >= o) ? buf[src][t - o] : 0);
-        buf[src ^ 1][t] = x;
-        src ^= 1;
-        __syncthreads();
+    const int per = (n + 63) / 64;
+    const int b0 = lane * per;
+    int sum = 0;
+    for (int i = 0; i < per; ++i)
+        if (b0 + i < n) sum += a[b0 + i];
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += v;
     }
-    const int incl = buf[src][t];
-    if (t < n) a[t] = incl - v;
-    if (t == n - 1) a[n] = incl;
-    if (t == 0 && n == 0) a[0] = 0;
-    __syncthreads();
+    int run = incl - sum;
+    for (int i = 0; i < per; ++i)
+        if (b0 + i < n) {
+            const int v = a[b0 + i];
+            a[b0 + i] = run;
+            run += v;
+        }
+    if (lane == 63) a[n] = incl;
 }
 
-__global__ __launch_bounds__(1024) void moe_prepare_kernel(MoeParams p)
+// Slot activity (exl3_moe_coop_kernel.cuh:208-223) -> local[s] = local expert or -1 (bounds
+// violations set the sticky flag and make the slot inactive), then the stable order of the
+// active slots by (expert, slot) and, when publishing, the reference run table.
+template <typename SelT>
+__device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* rw, int slots, int* local,
+                            int* order, ExpertLds& ex, bool publish)
 {
-    __shared__ PrepShared sh;
-    const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    const int slots = p.T * p.topk;
+    const int t = threadIdx.x, nt = blockDim.x, lane = t & 63, wave = t >> 6;
     const int E = p.n_local;
-
-    // --- routing -------------------------------------------------------------------------
-    if (p.logits) {
-        for (int r = wave; r < p.T; r += 16) {
-            const float* z = p.logits + (size_t)r * p.n_logits;
-            float key[EVAMX_MAX_EXPERTS / 64];
-            int nper = (p.n_logits + 63) / 64;
-#pragma unroll
-            for (int i = 0; i < EVAMX_MAX_EXPERTS / 64; ++i) {
-                const int e = lane + 64 * i;
-                float k = -INFINITY;
-                if (i < nper && e < p.n_logits) {
-                    const float zz = z[e];
-                    if (p.sel_bias) k = score_fn(zz, p.score) + p.sel_bias[e];
-                    else k = (p.score == EVAMX_SCORE_SIGMOID) ? zz : score_fn(zz, p.score);
-                }
-                key[i] = k;
-            }
-            float tot = 0.0f;
-            float sc[EVAMX_MAX_TOPK];
-            int id[EVAMX_MAX_TOPK];
-            for (int j = 0; j < p.topk; ++j) {
-                float bk = -INFINITY;
-                int bi = 0x7fffffff;
-#pragma unroll
-                for (int i = 0; i < EVAMX_MAX_EXPERTS / 64; ++i) {
-                    const int e = lane + 64 * i;
-                    if (key[i] > bk || (key[i] == bk && e < bi)) { bk = key[i]; bi = e; }
-                }
-#pragma unroll
-                for (int m = 1; m < 64; m <<= 1) {
-                    const float ok = __shfl_xor(bk, m, WAVE);
-                    const int oi = __shfl_xor(bi, m, WAVE);
-                    if (ok > bk || (ok == bk && oi < bi)) { bk = ok; bi = oi; }
-                }
-#pragma unroll
-                for (int i = 0; i < EVAMX_MAX_EXPERTS / 64; ++i)
-                    if (lane + 64 * i == bi) key[i] = -INFINITY;
-                id[j] = bi;
-                sc[j] = score_fn(z[bi], p.score);
-                tot = tot + sc[j];
-            }
-            if (lane == 0) {
-                for (int j = 0; j < p.topk; ++j) {
-                    float w = sc[j] / (tot + 1e-20f);
-                    w = w * p.route_scale;
-                    p.sel[(size_t)r * p.topk + j] = id[j];
-                    p.weights[(size_t)r * p.topk + j] = w;
-                    p.rw16[(size_t)r * p.topk + j] = f2h(w);
-                }
-            }
-        }
-    } else if (p.weights) {
-        for (int s = t; s < slots; s += 1024) p.rw16[s] = f2h(p.weights[s]);
-    }
-    if (!(p.mode & PREP_GROUP)) return;
+    for (int e = t; e < E; e += nt) { ex.cnt[e] = 0; ex.fill[e] = 0; }
     __syncthreads();
-
-    // --- activity, bounds, histogram ----------------------------------------------------------
-    for (int e = t; e < EVAMX_MAX_EXPERTS; e += 1024) sh.cnt[e] = 0;
-    if (t == 0) sh.n_active = 0;
-    __syncthreads();
-    for (int s = t; s < slots; s += 1024) {
-        const int64_t e = p.sel[s];
-        const float w = h2f(p.rw16[s]);
-        int local = -1;
+    for (int s = t; s < slots; s += nt) {
+        const int64_t e = (int64_t)sel[s];
+        const float w = h2f(rw[s]);
+        int lo = -1;
         if (w != 0.0f) {
             int64_t le = e;
             bool ok = true;
@@ -191,126 +230,100 @@ __global__ __launch_bounds__(1024) void moe_prepare_kernel(MoeParams p)
                 le = e - p.min_expert;
             }
             if (ok) {
-                if (le < 0 || le >= E) atomicOr(p.err, EVAMX_ERR_EXPERT_RANGE);
-                else local = (int)le;
+                if (le < 0 || le >= E) {
+                    if (publish) atomicOr(p.err, EVAMX_ERR_EXPERT_RANGE);
+                } else lo = (int)le;
             }
         }
-        p.local[s] = local;
-        if (local >= 0) atomicAdd(&sh.cnt[local], 1);
+        local[s] = lo;
+        if (lo >= 0) atomicAdd(&ex.cnt[lo], 1);
     }
     __syncthreads();
-
-    // --- per-expert offsets, run bases (runs of <= 8), chunk bases (chunks of <= CHUNK) -------
-    for (int e = t; e < E; e += 1024) {
-        sh.off[e] = sh.cnt[e];
-        sh.run_base[e] = (sh.cnt[e] + 7) / 8;
-        sh.chunk_base[e] = (sh.cnt[e] + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
+    if (wave == 0) {
+        for (int e = lane; e < E; e += 64) {
+            ex.off[e] = ex.cnt[e];
+            ex.run_base[e] = (ex.cnt[e] + 7) / 8;
+            ex.chunk_base[e] = (ex.cnt[e] + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
+        }
+        wave_excl_scan(ex.off, E, lane);
+        wave_excl_scan(ex.run_base, E, lane);
+        wave_excl_scan(ex.chunk_base, E, lane);
+        // Stable scatter by (expert, slot): blocks of 64 slots in order; lanes holding the same
+        // expert find each other with one ballot per expert-index bit.
+        for (int s0 = 0; s0 < slots; s0 += 64) {
+            const int s = s0 + lane;
+            const int e = s < slots ? local[s] : -1;
+            const bool act = e >= 0;
+            uint64_t m = __ballot(act);
+#pragma unroll
+            for (int b = 0; b < 10; ++b) {
+                const bool bit = act && ((e >> b) & 1);
+                const uint64_t bb = __ballot(bit);
+                m &= bit ? bb : ~bb;
+            }
+            const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+            int rank = 0;
+            if (act) {
+                rank = ex.fill[e] + __popcll(m & lt);
+                const int pos = ex.off[e] + rank;
+                if (order) order[pos] = s;
+                if (publish && p.runs) {
+                    p.runs[2 + p.slots_max + 1 + pos] = s;
+                    if ((rank & 7) == 0) p.runs[2 + ex.run_base[e] + rank / 8] = pos;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (act && (m & lt) == 0) ex.fill[e] += __popcll(m);
+            __builtin_amdgcn_wave_barrier();
+        }
     }
     __syncthreads();
-    block_exclusive_scan(sh.off, E);
-    block_exclusive_scan(sh.run_base, E);
-    block_exclusive_scan(sh.chunk_base, E);
-    const int n_active = sh.off[E];
-    const int n_runs = sh.run_base[E];
-    const int n_routed_chunks = sh.chunk_base[E];
+}
 
-    // --- run table (zeroed, then filled) and the sorted order ---------------------------------
-    const int table_len = 2 + 2 * p.slots_max + 1;
-    for (int i = t; i < table_len; i += 1024) p.runs[i] = 0;
-    __syncthreads();
-    int* run_start = p.runs + 2;
-    int* order = p.runs + 2 + p.slots_max + 1;
-    for (int s = t; s < slots; s += 1024) {
-        const int e = p.local[s];
-        if (e < 0) continue;
-        int rank = 0;                                  // earlier active slots of the same expert
-        for (int u = 0; u < s; ++u) rank += (p.local[u] == e) ? 1 : 0;
-        const int pos = sh.off[e] + rank;
-        order[pos] = s;
-        if (p.order) p.order[pos] = s;
-        if ((rank & 7) == 0) run_start[sh.run_base[e] + rank / 8] = pos;
-    }
-    if (t == 0) {
-        p.runs[0] = n_runs;
-        p.runs[1] = 0;
-        run_start[n_runs] = n_active;
-    }
-    if (!p.order) return;                             // run table only (prepare_routes)
-    // shared-expert slots follow the routed ones in the chunk order
-    if (p.has_shared)
-        for (int r = t; r < p.T; r += 1024) p.order[n_active + r] = slots + r;
-
-    // --- chunks ----------------------------------------------------------------------------
-    for (int e = t; e < E; e += 1024) {
-        const int n = sh.cnt[e];
+// Chunks of <= EVAMX_CHUNK slots per expert, then the shared expert's rows.
+__device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, int* chunks)
+{
+    const int t = threadIdx.x, nt = blockDim.x;
+    const int E = p.n_local;
+    const int n_active = ex.off[E];
+    for (int e = t; e < E; e += nt) {
+        const int n = ex.cnt[e];
         for (int j = 0; j * EVAMX_CHUNK < n; ++j) {
-            int* c = p.chunks + 4 * (sh.chunk_base[e] + j);
+            int* c = chunks + 4 * (ex.chunk_base[e] + j);
             c[0] = e;
-            c[1] = sh.off[e] + j * EVAMX_CHUNK;
+            c[1] = ex.off[e] + j * EVAMX_CHUNK;
             c[2] = min(EVAMX_CHUNK, n - j * EVAMX_CHUNK);
             c[3] = p.k2_per_expert ? (int)p.k2_per_expert[e] : p.k2_uniform;
         }
     }
-    int n_chunks = n_routed_chunks;
     if (p.has_shared) {
+        const int base = ex.chunk_base[E];
         const int nsc = (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
-        for (int j = t; j < nsc; j += 1024) {
-            int* c = p.chunks + 4 * (n_routed_chunks + j);
+        for (int j = t; j < nsc; j += nt) {
+            int* c = chunks + 4 * (base + j);
             c[0] = -1;
             c[1] = n_active + j * EVAMX_CHUNK;
             c[2] = min(EVAMX_CHUNK, p.T - j * EVAMX_CHUNK);
             c[3] = p.k2_shared;
         }
-        n_chunks += nsc;
-    }
-    if (t == 0) {
-        p.meta[0] = n_chunks;
-        p.meta[1] = n_active;
-    }
-    if (!(p.mode & PREP_MOE)) return;
-
-    // --- counters, per-token arrival counts, empty rows ---------------------------------------
-    for (int i = t; i < p.ctr_gu_len; i += 1024) p.ctr_gu[i] = 0;
-    for (int i = t; i < p.ctr_d_len; i += 1024) p.ctr_d[i] = 0;
-    __syncthreads();
-    for (int r = t; r < p.T; r += 1024) {
-        int n = p.has_shared ? 1 : 0;
-        for (int k = 0; k < p.topk; ++k) n += (p.local[r * p.topk + k] >= 0) ? 1 : 0;
-        p.tok_cnt[r] = n;
-    }
-    __syncthreads();
-    for (int i = t; i < p.T * p.H; i += 1024) {
-        const int r = i / p.H;
-        if (p.tok_cnt[r] == 0) p.out[(size_t)r * p.out_stride + (i % p.H)] = 0.0f;
     }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Input rotation: one wave per (slot, 128-chunk, gate|up).
-
-__global__ __launch_bounds__(256) void moe_rotate_kernel(MoeParams p)
+__device__ __forceinline__ int total_chunks(const MoeParams& p, const ExpertLds& ex)
 {
-    const int lane = threadIdx.x & 63;
-    const int item = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int nch = p.H / 128;
+    return ex.chunk_base[p.n_local] + (p.has_shared ? (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Input rotation of one (slot, 128-chunk, gate|up) item by one wave.
+
+__device__ void rotate_item(const MoeParams& p, int s, int e, int c, int proj, int lane)
+{
     const int slots = p.T * p.topk;
-    const int nslot = slots + (p.has_shared ? p.T : 0);
-    if (item >= nslot * nch * 2) return;
-    const int s = item / (nch * 2);
-    const int rem = item % (nch * 2);
-    const int c = rem >> 1, proj = rem & 1;
     const bool shared = s >= slots;
-    int row;
-    const half_t* suh;
-    if (shared) {
-        row = s - slots;
-        suh = (const half_t*)p.sh_ptr[proj == 0 ? EVAMX_TBL_G_SUH : EVAMX_TBL_U_SUH];
-    } else {
-        const int e = p.local[s];
-        if (e < 0) return;
-        row = s / p.topk;
-        suh = (const half_t*)p.tables[(size_t)(proj == 0 ? EVAMX_TBL_G_SUH : EVAMX_TBL_U_SUH) * p.tbl_stride + e];
-    }
+    const int row = shared ? s - slots : s / p.topk;
+    const int trow = proj == 0 ? EVAMX_TBL_G_SUH : EVAMX_TBL_U_SUH;
+    const half_t* suh = shared ? (const half_t*)p.sh_ptr[trow] : (const half_t*)p.tables[(size_t)trow * p.tbl_stride + e];
     float v[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -323,9 +336,131 @@ __global__ __launch_bounds__(256) void moe_rotate_kernel(MoeParams p)
     }
     had128_lane(v[0], v[1], lane);
     half_t* dst = p.xr + ((size_t)proj * p.nslot_max + s) * p.H + c * 128;
-    dst[lane_col(lane, 0)] = f2h(v[0]);
-    dst[lane_col(lane, 1)] = f2h(v[1]);
+    const half_t r0 = f2h(v[0]), r1 = f2h(v[1]);
+    dst[lane_col(lane, 0)] = r0;
+    dst[lane_col(lane, 1)] = r1;
+    const float sum = wave_sum(h2f(r0) + h2f(r1));
+    if (lane == 0) p.xsum[((size_t)proj * p.nslot_max + s) * (p.H / 128) + c] = sum;
 }
+
+// ---------------------------------------------------------------------------------------------
+// Prepare for small batches (T*topk <= EVAMX_SMALL_SLOTS, T <= EVAMX_CHUNK): every workgroup
+// routes and groups in LDS, workgroup 0 publishes, then all workgroups rotate.
+
+constexpr int EVAMX_SMALL_SLOTS = 512;
+
+struct SmallLds {
+    ExpertLds ex;
+    int sel[EVAMX_SMALL_SLOTS];
+    half_t rw[EVAMX_SMALL_SLOTS];
+    int local[EVAMX_SMALL_SLOTS];
+    int order[EVAMX_SMALL_SLOTS + EVAMX_CHUNK];
+};
+
+__global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
+{
+    __shared__ SmallLds sh;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int slots = p.T * p.topk;
+    const bool pub = blockIdx.x == 0;
+    if (p.logits) {
+        for (int r = wave; r < p.T; r += 4) route_token(p, r, lane, sh.sel, sh.rw, pub);
+    } else {
+        for (int s = t; s < slots; s += 256) {
+            const int64_t e = p.sel[s];
+            // indices outside the int range are outside any table: keep them out of range
+            sh.sel[s] = (e >= 0 && e < 0x7fffffff) ? (int)e : -1;
+            sh.rw[s] = p.weights ? f2h(p.weights[s]) : p.rw16[s];
+            if (pub && p.weights) p.rw16[s] = sh.rw[s];
+        }
+    }
+    if (pub && p.runs) {
+        const int table_len = 2 + 2 * p.slots_max + 1;
+        for (int i = t; i < table_len; i += 256) p.runs[i] = 0;
+    }
+    __syncthreads();
+    group_slots(p, sh.sel, sh.rw, slots, sh.local, sh.order, sh.ex, pub);
+    const int n_active = sh.ex.off[p.n_local];
+    if (p.has_shared)
+        for (int r = t; r < p.T; r += 256) sh.order[n_active + r] = slots + r;
+    __syncthreads();
+    if (pub) {
+        for (int s = t; s < slots; s += 256) p.local[s] = sh.local[s];
+        for (int i = t; i < n_active + (p.has_shared ? p.T : 0); i += 256) p.order[i] = sh.order[i];
+        write_chunks(p, sh.ex, p.chunks);
+        if (t == 0) {
+            p.runs[0] = sh.ex.run_base[p.n_local];
+            p.runs[1] = 0;
+            p.runs[2 + sh.ex.run_base[p.n_local]] = n_active;
+            p.meta[0] = total_chunks(p, sh.ex);
+            p.meta[1] = n_active;
+        }
+    }
+    // rotations: items (o, chunk, proj) over the grouped order, grid-stride by wave
+    const int nch = p.H / 128;
+    const int n_items = (n_active + (p.has_shared ? p.T : 0)) * nch * 2;
+    for (int it = blockIdx.x * 4 + wave; it < n_items; it += gridDim.x * 4) {
+        const int o = it / (nch * 2);
+        const int rem = it % (nch * 2);
+        const int s = sh.order[o];
+        rotate_item(p, s, s < slots ? sh.local[s] : -1, rem >> 1, rem & 1, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Prepare for any batch: one workgroup of 1024 threads with the per-slot arrays in global
+// memory. Mode bits select routing only, routing + run table, or the whole MoE prologue except
+// the rotation (moe_rotate_kernel follows).
+
+__global__ __launch_bounds__(1024) void moe_prepare_large_kernel(MoeParams p)
+{
+    __shared__ ExpertLds ex;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int slots = p.T * p.topk;
+    if (p.logits) {
+        for (int r = wave; r < p.T; r += 16) route_token(p, r, lane, nullptr, nullptr, true);
+    } else if (p.weights) {
+        for (int s = t; s < slots; s += 1024) p.rw16[s] = f2h(p.weights[s]);
+    }
+    if (!(p.mode & PREP_GROUP)) return;
+    if (p.runs) {
+        const int table_len = 2 + 2 * p.slots_max + 1;
+        for (int i = t; i < table_len; i += 1024) p.runs[i] = 0;
+    }
+    __syncthreads();
+    group_slots(p, p.sel, p.rw16, slots, p.local, p.order, ex, true);
+    const int n_active = ex.off[p.n_local];
+    if (t == 0 && p.runs) {
+        p.runs[0] = ex.run_base[p.n_local];
+        p.runs[1] = 0;
+        p.runs[2 + ex.run_base[p.n_local]] = n_active;
+    }
+    if (!(p.mode & PREP_MOE)) return;
+    if (p.has_shared)
+        for (int r = t; r < p.T; r += 1024) p.order[n_active + r] = slots + r;
+    write_chunks(p, ex, p.chunks);
+    if (t == 0) {
+        p.meta[0] = total_chunks(p, ex);
+        p.meta[1] = n_active;
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_rotate_kernel(MoeParams p)
+{
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nch = p.H / 128;
+    const int slots = p.T * p.topk;
+    const int n_rows = p.meta[1] + (p.has_shared ? p.T : 0);
+    for (int it = wid; it < n_rows * nch * 2; it += gridDim.x * 4) {
+        const int o = it / (nch * 2);
+        const int rem = it % (nch * 2);
+        const int s = p.order[o];
+        rotate_item(p, s, s < slots ? p.local[s] : -1, rem >> 1, rem & 1, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 
 __device__ __forceinline__ const void* expert_ptr(const MoeParams& p, int e, int row)
 {
@@ -333,21 +468,18 @@ __device__ __forceinline__ const void* expert_ptr(const MoeParams& p, int e, int
     return (const void*)p.tables[(size_t)row * p.tbl_stride + e];
 }
 
-// ---------------------------------------------------------------------------------------------
-// Gate/up GEMV + activation epilogue.
-
-__global__ __launch_bounds__(256) void moe_gemv_gu_kernel(MoeParams p, const half_t* __restrict__ xr)
+// Gate/up GEMV: per wave (chunk, 128 columns, gate|up, k-split) -> part_gu[ks][proj][slot][I].
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_kernel(MoeParams p, const half_t* __restrict__ xr)
 {
-    const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int ncg = p.I / 128;
     const int S = p.ks_gu;
     const int c = wid / (2 * ncg * S);
     if (c >= p.meta[0]) return;
     int rem = wid % (2 * ncg * S);
-    const int proj = rem / (ncg * S);
-    rem %= ncg * S;
-    const int cg = rem / S, ks = rem % S;
+    const int cg = rem / (2 * S);
+    rem %= 2 * S;
+    const int proj = rem / S, ks = rem % S;
 
     const int* ch = p.chunks + 4 * c;
     const int e = __builtin_amdgcn_readfirstlane(ch[0]);
@@ -356,79 +488,104 @@ __global__ __launch_bounds__(256) void moe_gemv_gu_kernel(MoeParams p, const hal
     const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
     const int* slot_of = p.order + begin;
 
-    const int kt_n = p.H / 16;
-    const int kt0 = kt_n * ks / S, kt1 = kt_n * (ks + 1) / S;
+    const int nch = p.H / 128;
+    const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
     const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, proj == 0 ? EVAMX_TBL_G_TRELLIS : EVAMX_TBL_U_TRELLIS);
-    const half_t* A = xr + (size_t)proj * p.nslot_max * p.H;
+    const GlobalRows src{xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch,
+                         nch};
     float* part = p.part_gu + ((size_t)ks * 2 + proj) * p.nslot_max * p.I;
-    gemv_dispatch_k(k2, trellis, p.I / 16, cg, kt0, kt1, A, (size_t)p.H, slot_of, tm, part, (size_t)p.I);
+    gemv_dispatch_k(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
+}
 
-    if (!arrive_last(p.ctr_gu + (size_t)c * ncg + cg, 2 * S)) return;
-
-    // Epilogue for the chunk's slots on columns cg*128 .. +127.
+// Activation epilogue: one wave per (grouped row o, 128-chunk a of I). Sums the gate/up
+// partials in fixed order, rounds to fp16 (gu_f32 = false), then exl3_moe_coop_kernel.cuh:
+// 784-805 for routed slots (act_gate with the clamp after SiLU) or the shared expert's EXL3
+// linear outputs + swiglu (model.py:450-452, kernels.py:213-217), and the down projection's
+// input rotation; writes act (fp16) and the chunk's sum.
+__global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
+{
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int na = p.I / 128;
+    const int n_rows = p.meta[1] + (p.has_shared ? p.T : 0);
+    if (wid >= n_rows * na) return;
+    const int o = wid / na, a = wid % na;
+    const int slots = p.T * p.topk;
+    const int s = __builtin_amdgcn_readfirstlane(p.order[o]);
+    const int e = s < slots ? __builtin_amdgcn_readfirstlane(p.local[s]) : -1;
     const bool shared = e < 0;
     const half_t* g_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_G_SVH);
     const half_t* u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
     const half_t* d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
     const float L = p.limit;
-    for (int m = 0; m < tm; ++m) {
-        const int s = slot_of[m];
-        float g[2], u[2];
+    const int Sg = p.ks_gu;
+    float g[2], u[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int col = cg * 128 + lane_col(lane, h);
-            float sg = 0.0f, su = 0.0f;
-            for (int q = 0; q < S; ++q) {
-                sg += p.part_gu[(((size_t)q * 2 + 0) * p.nslot_max + s) * p.I + col];
-                su += p.part_gu[(((size_t)q * 2 + 1) * p.nslot_max + s) * p.I + col];
-            }
-            g[h] = h2f(f2h(sg));     // GEMV output stored as fp16 (gu_f32 = false)
-            u[h] = h2f(f2h(su));
-        }
-        had128_lane(g[0], g[1], lane);
-        had128_lane(u[0], u[1], lane);
-        float a[2];
+    for (int h = 0; h < 2; ++h) {
+        const int col = a * 128 + lane_col(lane, h);
+        const float* pg = p.part_gu + (size_t)s * p.I + col;
+        const size_t pstride = (size_t)2 * p.nslot_max * p.I;        // next k-split
+        const size_t ustride = (size_t)p.nslot_max * p.I;            // gate -> up
+        float sg = 0.0f, su = 0.0f;
+        int q = 0;
+        for (; q + 4 <= Sg; q += 4) {
+            float tg[4], tu[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int col = cg * 128 + lane_col(lane, h);
-            const float gs = h2f(g_svh[col]), us = h2f(u_svh[col]), ds = h2f(d_suh[col]);
-            float gv, uv, x;
-            if (shared) {
-                // EXL3 linear outputs: fp16 after the rotation, fp16 product with svh
-                gv = h2f(f2h(h2f(f2h(g[h])) * gs));
-                uv = h2f(f2h(h2f(f2h(u[h])) * us));
-                // swiglu: clamp the gate BEFORE SiLU (kernels.py:213-217), mid to fp16, fp16
-                // product with the down projection's suh
-                if (L > 0.0f) {
-                    uv = fminf(fmaxf(uv, -L), L);
-                    gv = fminf(gv, L);
-                }
-                const float mid = h2f(f2h(silu_f(gv) * uv));
-                a[h] = h2f(f2h(mid * ds));
-            } else {
-                gv = g[h] * gs;
-                uv = u[h] * us;
-                x = silu_f(gv);
-                if (L != 0.0f) {
-                    uv = fminf(fmaxf(uv, -L), L);
-                    x = fminf(x, L);
-                }
-                a[h] = x * uv * ds;
+            for (int i = 0; i < 4; ++i) {
+                tg[i] = pg[(q + i) * pstride];
+                tu[i] = pg[(q + i) * pstride + ustride];
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { sg += tg[i]; su += tu[i]; }
         }
-        had128_lane(a[0], a[1], lane);
-        half_t* dst = p.act + (size_t)s * p.I + cg * 128;
-        dst[lane_col(lane, 0)] = f2h(a[0]);
-        dst[lane_col(lane, 1)] = f2h(a[1]);
+        for (; q < Sg; ++q) {
+            sg += pg[q * pstride];
+            su += pg[q * pstride + ustride];
+        }
+        g[h] = h2f(f2h(sg));     // GEMV output stored as fp16 (gu_f32 = false)
+        u[h] = h2f(f2h(su));
     }
+    had128_lane(g[0], g[1], lane);
+    had128_lane(u[0], u[1], lane);
+    float av[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int col = a * 128 + lane_col(lane, h);
+        const float gs = h2f(g_svh[col]), us = h2f(u_svh[col]), ds = h2f(d_suh[col]);
+        if (shared) {
+            // EXL3 linear outputs: fp16 after the rotation, fp16 product with svh; swiglu clamps
+            // the gate BEFORE SiLU; mid to fp16; fp16 product with the down projection's suh
+            float gv = h2f(f2h(h2f(f2h(g[h])) * gs));
+            float uv = h2f(f2h(h2f(f2h(u[h])) * us));
+            if (L > 0.0f) {
+                uv = fminf(fmaxf(uv, -L), L);
+                gv = fminf(gv, L);
+            }
+            const float mid = h2f(f2h(silu_f(gv) * uv));
+            av[h] = h2f(f2h(mid * ds));
+        } else {
+            const float gv = g[h] * gs;
+            float uv = u[h] * us;
+            float x = silu_f(gv);
+            if (L != 0.0f) {
+                uv = fminf(fmaxf(uv, -L), L);
+                x = fminf(x, L);
+            }
+            av[h] = x * uv * ds;
+        }
+    }
+    had128_lane(av[0], av[1], lane);
+    half_t* dst = p.act + (size_t)s * p.I + a * 128;
+    const half_t r0 = f2h(av[0]), r1 = f2h(av[1]);
+    dst[lane_col(lane, 0)] = r0;
+    dst[lane_col(lane, 1)] = r1;
+    const float sum = wave_sum(h2f(r0) + h2f(r1));
+    if (lane == 0) p.actsum[(size_t)s * na + a] = sum;
 }
 
-// ---------------------------------------------------------------------------------------------
-// Down GEMV + per-token slot reduction.
-
-__global__ __launch_bounds__(256) void moe_gemv_down_kernel(MoeParams p, const half_t* __restrict__ act)
+// Down GEMV: per wave (chunk, 128 columns, k-split) -> part_d[ks][slot][H].
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_down_kernel(MoeParams p, const half_t* __restrict__ act)
 {
-    const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int ncg = p.H / 128;
     const int S = p.ks_d;
@@ -444,62 +601,95 @@ __global__ __launch_bounds__(256) void moe_gemv_down_kernel(MoeParams p, const h
     const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
     const int* slot_of = p.order + begin;
 
-    const int kt_n = p.I / 16;
-    const int kt0 = kt_n * ks / S, kt1 = kt_n * (ks + 1) / S;
+    const int na = p.I / 128;
+    const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
     const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, EVAMX_TBL_D_TRELLIS);
     float* part = p.part_d + (size_t)ks * p.nslot_max * p.H;
-    gemv_dispatch_k(k2, trellis, p.H / 16, cg, kt0, kt1, act, (size_t)p.I, slot_of, tm, part, (size_t)p.H);
+    gemv_dispatch_k(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{act, (size_t)p.I, p.actsum, na}, slot_of, tm, part,
+                    (size_t)p.H);
+}
 
+// Sum of the down k-split partials of slot s on this lane's two columns, fixed order; loads of
+// four splits are issued before their adds.
+__device__ __forceinline__ void sum_partials(const MoeParams& p, int s, int cg, int lane, int S, float (&v)[2])
+{
+    const size_t stride = (size_t)p.nslot_max * p.H;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float* pp = p.part_d + (size_t)s * p.H + cg * 128 + lane_col(lane, h);
+        float acc = 0.0f;
+        int q = 0;
+        for (; q + 4 <= S; q += 4) {
+            float t[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t[i] = pp[(q + i) * stride];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc += t[i];
+        }
+        for (; q < S; ++q) acc += pp[q * stride];
+        v[h] = acc;
+    }
+}
+
+// Per-token reduction over slots in slot order (+ shared expert). One workgroup of 4 waves per
+// (token, 128 columns): wave w handles slots w, w+4, ... (output rotation * svh * weight) into
+// LDS, then wave 0 sums them in slot order, as the reference sums one warp per slot
+// (exl3_moe_coop_kernel.cuh:906-940), and adds the shared expert.
+__global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
+{
+    __shared__ float part[EVAMX_MAX_TOPK + 1][128];
+    __shared__ int active[EVAMX_MAX_TOPK + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ncg = p.H / 128;
+    const int row = blockIdx.x / ncg, cg = blockIdx.x % ncg;
     const int slots = p.T * p.topk;
-    for (int m = 0; m < tm; ++m) {
-        const int s = slot_of[m];
-        const int row = (s < slots) ? s / p.topk : s - slots;
-        if (!arrive_last(p.ctr_d + (size_t)row * ncg + cg, p.tok_cnt[row] * S)) continue;
-
-        float o[2] = {0.0f, 0.0f};
+    const int S = p.ks_d;
+    const int c0 = lane_col(lane, 0), c1 = lane_col(lane, 1);
+    const int col0 = cg * 128 + c0, col1 = cg * 128 + c1;
+    const int nitems = p.topk + (p.has_shared ? 1 : 0);
+    for (int k = wave; k < nitems; k += 4) {
+        const bool shared = k == p.topk;
+        const int sk = shared ? slots + row : row * p.topk + k;
+        const int le = shared ? -1 : p.local[sk];
+        if (!shared && le < 0) {
+            if (lane == 0) active[k] = 0;
+            continue;
+        }
+        const half_t* svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
+                                   : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
+        const float w = shared ? 1.0f : h2f(p.rw16[sk]);
+        const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
+        float v[2];
+        sum_partials(p, sk, cg, lane, S, v);
+        if (shared) {
+            v[0] = h2f(f2h(v[0]));                     // EXL3 linear C in fp16
+            v[1] = h2f(f2h(v[1]));
+        }
+        had128_lane(v[0], v[1], lane);
+        if (shared) {
+            part[k][c0] = h2f(f2h(h2f(f2h(v[0])) * s0));
+            part[k][c1] = h2f(f2h(h2f(f2h(v[1])) * s1));
+        } else {
+            part[k][c0] = w * (v[0] * s0);
+            part[k][c1] = w * (v[1] * s1);
+        }
+        if (lane == 0) active[k] = 1;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float o0 = 0.0f, o1 = 0.0f;
         for (int k = 0; k < p.topk; ++k) {
-            const int sk = row * p.topk + k;
-            const int le = p.local[sk];
-            if (le < 0) continue;
-            const float w = h2f(p.rw16[sk]);
-            const half_t* svh = (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
-            float v[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int col = cg * 128 + lane_col(lane, h);
-                float acc = 0.0f;
-                for (int q = 0; q < S; ++q) acc += p.part_d[((size_t)q * p.nslot_max + sk) * p.H + col];
-                v[h] = acc;
-            }
-            had128_lane(v[0], v[1], lane);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int col = cg * 128 + lane_col(lane, h);
-                o[h] = o[h] + w * (v[h] * h2f(svh[col]));
-            }
+            if (!active[k]) continue;
+            o0 = o0 + part[k][c0];
+            o1 = o1 + part[k][c1];
         }
         if (p.has_shared) {
-            const int ss = slots + row;
-            const half_t* svh = (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH];
-            float v[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int col = cg * 128 + lane_col(lane, h);
-                float acc = 0.0f;
-                for (int q = 0; q < S; ++q) acc += p.part_d[((size_t)q * p.nslot_max + ss) * p.H + col];
-                v[h] = h2f(f2h(acc));                      // EXL3 linear C in fp16
-            }
-            had128_lane(v[0], v[1], lane);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int col = cg * 128 + lane_col(lane, h);
-                const float y = h2f(f2h(h2f(f2h(v[h])) * h2f(svh[col])));
-                o[h] = o[h] + y;
-            }
+            o0 = o0 + part[p.topk][c0];
+            o1 = o1 + part[p.topk][c1];
         }
-        float* dst = p.out + (size_t)row * p.out_stride + cg * 128;
-        dst[lane_col(lane, 0)] = o[0];
-        dst[lane_col(lane, 1)] = o[1];
+        float* dst = p.out + (size_t)row * p.out_stride;
+        dst[col0] = o0;
+        dst[col1] = o1;
     }
 }
 
@@ -508,27 +698,43 @@ __global__ __launch_bounds__(256) void moe_gemv_down_kernel(MoeParams p, const h
 
 int moe_prepare_only(MoeParams& p, hipStream_t stream)
 {
-    hipLaunchKernelGGL(moe_prepare_kernel, dim3(1), dim3(1024), 0, stream, p);
+    hipLaunchKernelGGL(moe_prepare_large_kernel, dim3(1), dim3(1024), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int moe_launch(MoeParams& p, hipStream_t stream)
+bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T <= EVAMX_CHUNK; }
+
+int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
 {
-    hipLaunchKernelGGL(moe_prepare_kernel, dim3(1), dim3(1024), 0, stream, p);
+    auto mark = [&](int i) {
+        if (events) (void)hipEventRecord((hipEvent_t)events[i], stream);
+    };
     const int nch = p.H / 128;
     const int nslot = p.T * p.topk + (p.has_shared ? p.T : 0);
-    {
-        const int waves = nslot * nch * 2;
-        hipLaunchKernelGGL(moe_rotate_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+    mark(0);
+    if (moe_small_path(p.T, p.topk)) {
+        int blocks = (nslot * nch * 2 + 3) / 4;
+        if (blocks > 256) blocks = 256;
+        hipLaunchKernelGGL(moe_prepare_small_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(moe_prepare_large_kernel, dim3(1), dim3(1024), 0, stream, p);
+        hipLaunchKernelGGL(moe_rotate_kernel, dim3(256), dim3(256), 0, stream, p);
     }
+    mark(1);
     {
         const int waves = p.max_chunks * 2 * (p.I / 128) * p.ks_gu;
-        hipLaunchKernelGGL(moe_gemv_gu_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.xr);
+        hipLaunchKernelGGL(moe_gate_up_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.xr);
     }
+    mark(2);
     {
-        const int waves = p.max_chunks * (p.H / 128) * p.ks_d;
-        hipLaunchKernelGGL(moe_gemv_down_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.act);
+        const int waves = nslot * (p.I / 128);
+        hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        const int dwaves = p.max_chunks * (p.H / 128) * p.ks_d;
+        hipLaunchKernelGGL(moe_down_kernel, dim3((dwaves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.act);
     }
+    mark(3);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(256), 0, stream, p);
+    mark(4);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

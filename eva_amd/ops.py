@@ -132,12 +132,14 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
                 logits: torch.Tensor | None = None, sel: torch.Tensor | None = None,
                 weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
                 score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
-                shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0):
+                shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0,
+                events=None):
     """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
 
     With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
     must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
     the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
+    ``events``: optional ctypes array of 5 hipEvent_t handles recorded around the launches.
     """
     s = ws.shape
     _dev(x, "x", None, 2)
@@ -179,6 +181,8 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     a.out_stride = out.stride(0)
     a.workspace = ptr(ws.buffer)
     a.workspace_bytes = ws.buffer.numel()
+    if events is not None:
+        a.events = ctypes.cast(events, ctypes.c_void_p)
     check(lib().evamx_moe_forward(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward")
     del keep
     return out

@@ -132,6 +132,9 @@ typedef struct evamx_moe_args {
     int32_t out_stride;           /* elements; >= hidden */
     void* workspace;              /* device, evamx_moe_workspace_bytes(&shape) bytes */
     size_t workspace_bytes;
+    /* optional: 5 hipEvent_t recorded before each of the 4 launches and after the last
+     * (per-launch timing on the launch stream); NULL for none */
+    void* const* events;
 } evamx_moe_args;
 
 size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape);
