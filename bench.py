@@ -107,11 +107,11 @@ def cpu_baseline(seconds_hint=True):
 
     run()                                   # warm-up
     times = []
-    for _ in range(3):
+    for _ in range(2):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
+    t = sum(times) / len(times)
     nbytes = 2 * expert_bytes(4)
     model = ""
     try:
@@ -120,7 +120,7 @@ def cpu_baseline(seconds_hint=True):
         pass
     return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"1 routed + 1 shared expert of the 1-token DSv3 layer at 4 bpw "
-                      f"({nbytes / 1e6:.1f} MB; median of 3 after 1 warm-up; {t:.2f} s each)",
+                      f"({nbytes / 1e6:.1f} MB; mean of 2 runs after 1 warm-up; {t:.2f} s each)",
             "layer_seconds_scaled": round(t * 9 / 2, 2), "cpu_model": model,
             "torch_threads": torch.get_num_threads()}
 
@@ -136,8 +136,12 @@ def main():
     ap.add_argument("--graph-steps", type=int, default=8)
     ap.add_argument("--ksplit-gu", type=int, default=0)
     ap.add_argument("--ksplit-down", type=int, default=0)
+    ap.add_argument("--routing", choices=("plain", "skewed"), default=None,
+                    help="N(0,1) logits, or config 3's per-token bias (default: plain at 1 token, skewed above)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, "
@@ -146,16 +150,30 @@ def main():
 
     import torch
 
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
+
     from eva_amd import ops
     from eva_amd._lib import lib
 
     dev = torch.device("cuda", 0)
     T = args.tokens
+    if args.routing is None:
+        args.routing = "plain" if T == 1 else "skewed"
     layers = DeviceLayers(torch, dev, args.layers, args.bits)
     g = torch.Generator(device=dev)
     g.manual_seed(99)
     n_draws = max(args.graph_steps, args.layers) * 2
     logits = torch.randn((n_draws, T, E), generator=g, device=dev)
+    if args.routing == "skewed":
+        # config 3: per-token random bias so expert loads span 0..T (2 hot experts +6 for every
+        # token, 6 warm experts +3 for a per-token coin flip, a fresh draw of both per step)
+        for i in range(n_draws):
+            perm = torch.randperm(E, generator=g, device=dev)
+            logits[i][:, perm[:2]] += 6.0
+            coin = torch.randint(0, 2, (T, 6), generator=g, device=dev).float()
+            logits[i][:, perm[2:8]] += 3.0 * coin
     x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
     ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
                           ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down)
@@ -226,7 +244,7 @@ def main():
                 "achieved": round(gu_bytes_launch / (gu_us * 1e-6) / 1e9, 1),
                 "peak": PEAK_HBM, "unit": "GB/s",
                 "frac": round(gu_bytes_launch / (gu_us * 1e-6) / 1e9 / PEAK_HBM, 4),
-                "traffic": None,
+                "traffic": measured_traffic(T, args.bits),
                 "algorithmic_bytes_per_launch": int(gu_bytes_launch),
                 "avg_launch_us": round(gu_us, 3)}
 
@@ -235,7 +253,9 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 6), "us_per_layer": round(us_step, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5)/sqrt(H) svh, N(0,1) logits, bf16 N(0,1) x)",
-        "config": {"workload": f"DSv3 MoE layer decode, {T} token(s), {args.bits:g} bpw EXL3 (BASELINE configs[1])",
+        "config": {"workload": f"DSv3 MoE layer decode, {T} token(s), {args.bits:g} bpw EXL3 "
+                               f"(BASELINE configs[{1 if T == 1 else 2}])", "routing": args.routing,
+                   "unique_experts_per_step": round(mean_uniq, 2),
                    "hidden": H, "inter": I, "experts": E, "shared": 1, "topk": TOPK, "tokens": T,
                    "bits": args.bits, "layers_cycled": args.layers, "graph": graph is not None,
                    "ksplit_gu": ws_ks(ws, 0), "ksplit_down": ws_ks(ws, 1)},
@@ -249,15 +269,46 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(torch):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch, against
+    COPY_BYTES, is the scale factor applied to the same counters of the MoE kernels."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "dispatches": 10}), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_gate_up_traffic_dsv3.md")
+
+
+def measured_traffic(tokens, bits):
+    """HBM bytes per moe_gate_up launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration), or None if this workload has
+    not been profiled."""
+    import re
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(rf"^traffic_bytes_per_launch\[tokens={tokens},bits={bits:g}\]:\s*(\d+)", text, flags=re.M)
+    return int(m.group(1)) if m else None
+
+
 def ws_ks(ws, which):
     return ws.shape.ksplit_gu if which == 0 else ws.shape.ksplit_down
 
 
 def kernel_times(torch, ops, lib, ws, x, layers, logits, sel, wts, out, args, stream, n_draws, n=64):
-    """Average duration of each of the four launches, from events recorded between them."""
-    from eva_amd import _lib
-    names = ["moe_prepare", "moe_gate_up", "moe_down", "moe_combine"]
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(n)]
+    """Average duration of each of the five stages, from hipEvents recorded between the launches
+    on the launch stream (eager steps cycling the resident layers)."""
+    names = ["moe_prepare", "moe_gate_up", "moe_act", "moe_down", "moe_combine"]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(n)]
     for row in evs:
         for e in row:
             e.record(stream)          # creates the underlying hipEvent
@@ -265,17 +316,17 @@ def kernel_times(torch, ops, lib, ws, x, layers, logits, sel, wts, out, args, st
     with torch.cuda.stream(stream):
         for i in range(n):
             l = i % args.layers
-            hs = (ctypes.c_void_p * 5)(*[e.cuda_event for e in evs[i]])
+            hs = (ctypes.c_void_p * 6)(*[e.cuda_event for e in evs[i]])
             handles.append(hs)
             ops.moe_forward(ws, x, layers.tables[l], out, limit=10.0, bits=args.bits, logits=logits[i % n_draws],
                             sel=sel, weights=wts, shared_ptrs=layers.shared[l], shared_bits=args.bits,
                             events=hs)
     torch.cuda.synchronize()
-    acc = [0.0] * 4
+    acc = [0.0] * 5
     for i in range(8, n):
-        for k in range(4):
+        for k in range(5):
             acc[k] += evs[i][k].elapsed_time(evs[i][k + 1])
-    return {names[k]: acc[k] * 1e3 / (n - 8) for k in range(4)}
+    return {names[k]: acc[k] * 1e3 / (n - 8) for k in range(5)}
 
 
 if __name__ == "__main__":

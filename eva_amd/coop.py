@@ -1,0 +1,316 @@
+"""Drop-in runners for eva's cooperative EXL3 MoE operator, on libevamx.
+
+Mirrors the reference's Python interface so callers switch by import:
+
+- ``CoopRunner(device, topk, hidden, inter, rows=1).run(x, sel, weights, packed, k, limit)``
+  -> borrowed fp32 ``[rows, hidden]`` (runtime/ds41/moe_coop.py:15-69);
+- ``CoopRunner512/2048/3072(device, topk=6, hidden=5120, inter=2304, max_rows=...)`` with
+  ``run(..., check_bounds=True)`` -> owned fp32 ``[M, hidden]``, ``prepare_routes``,
+  ``run_table``, ``lifecycle``, ``close`` (runtime/ds41/moe_coop3072.py:261-402,
+  moe_coop512.py:170-253, moe_coop2048.py:220-351), with their ownership rules: one owner
+  thread, the construction stream, a non-blocking lock, and any failure poisons the runner.
+
+Generalised as the DeepSeek-V3 shapes need: any hidden/inter (multiples of 128), top-k up to
+32, up to 512 local experts, rates 2/3/4/5 bits. ``packed`` is the ``[9, n_local]`` int64
+pointer table (rows g_trellis, g_suh, g_svh, u_trellis, u_suh, u_svh, d_trellis, d_suh,
+d_svh; runtime/ds41/cache.py:1877-1886) or a sequence of its 9 rows.
+
+Differences, all on the side of fewer host round trips:
+
+- bounds: the reference checks expert indices with a host synchronisation before launching
+  (csrc/moe_coop3072/moe_coop3072.cu:121-124). Here the kernels flag out-of-range experts in
+  the workspace and skip those slots; ``check_bounds=True`` reads the flag after the launch
+  (one synchronisation, as in the reference) and raises, poisoning the runner.
+  ``check_bounds=False`` skips the read and allows graph capture.
+- the run table is rebuilt by every ``run`` (as in the reference) and is the same int32 layout.
+"""
+from __future__ import annotations
+
+import math
+import threading
+
+import torch
+
+from . import ops
+
+RATES = (2, 3, 4, 5)
+
+
+def _pointer_table(packed, device, n_local=None):
+    """``[9, n]`` int64 device table from a tensor or a sequence of 9 row tensors."""
+    if isinstance(packed, torch.Tensor):
+        t = packed
+    elif isinstance(packed, (tuple, list)) and len(packed) == 9:
+        rows = list(packed)
+        if any(not isinstance(r, torch.Tensor) or r.ndim != 1 for r in rows):
+            raise ValueError("pointer table rows must be 1-D tensors")
+        base = rows[0]
+        n = base.numel()
+        contiguous_view = all(r.dtype == torch.int64 and r.numel() == n and r.stride(0) == 1
+                              and r.data_ptr() == base.data_ptr() + 8 * n * i for i, r in enumerate(rows))
+        t = (torch.as_strided(base, (9, n), (n, 1)) if contiguous_view else torch.stack(rows))
+    else:
+        raise ValueError("packed must be a [9, n_local] tensor or nine row tensors")
+    if t.ndim != 2 or t.shape[0] != 9 or t.dtype != torch.int64 or t.device != device:
+        raise ValueError("pointer table must be int64 [9, n_local] on the runner device")
+    if n_local is not None and t.shape[1] != n_local:
+        raise ValueError(f"pointer table has {t.shape[1]} experts, runner expects {n_local}")
+    return t.contiguous()
+
+
+def _check_rate(k):
+    if type(k) not in (int, float) or float(k) not in RATES:
+        raise ValueError(f"supported uniform rates are {RATES} bits")
+    return float(k)
+
+
+def _check_limit(limit):
+    if type(limit) not in (int, float) or not math.isfinite(limit) or not 0 <= limit <= 3.4028234663852886e38:
+        raise ValueError("limit must be a finite nonnegative float")
+    return float(limit)
+
+
+class CoopRunner:
+    """Fixed-row decode runner (runtime/ds41/moe_coop.py:15-69). ``run`` returns a borrowed
+    fp32 ``[rows, hidden]`` that the next call overwrites."""
+
+    def __init__(self, device, topk: int, hidden: int, inter: int, rows: int = 1, n_local: int | None = None):
+        slots = topk * rows
+        if rows < 1 or slots > 256:
+            raise ValueError("Cooperative EXL3 supports 1..256 routed slots")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("CoopRunner needs a GPU device")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.topk, self.rows, self.hi, self.inter, self.ho = topk, rows, hidden, inter, hidden
+        self.n_local = n_local
+        self._ws = {}
+        self.out = torch.empty(rows, hidden, device=self.device, dtype=torch.float32)
+        self.rw = torch.empty(rows, topk, device=self.device, dtype=torch.float16)
+
+    def _workspace(self, n_local):
+        ws = self._ws.get(n_local)
+        if ws is None:
+            ws = ops.MoeWorkspace(self.device, rows_max=self.rows, hidden=self.hi, inter=self.inter, topk=self.topk,
+                                  n_local=n_local, has_shared=False)
+            self._ws[n_local] = ws
+        return ws
+
+    def run(self, x, sel, weights, packed, k, limit) -> torch.Tensor:
+        table = _pointer_table(packed, self.device, self.n_local)
+        ws = self._workspace(table.shape[1])
+        x = x.reshape(self.rows, self.hi).contiguous()
+        if x.dtype not in (torch.float16, torch.bfloat16):
+            x = x.to(torch.float16)
+        sel = sel.reshape(self.rows, self.topk).to(dtype=torch.long).contiguous()
+        self.rw.copy_(weights.reshape(self.rows, self.topk).to(dtype=torch.float16))
+        ops.moe_forward(ws, x, table, self.out, limit=_check_limit(limit), bits=_check_rate(k), sel=sel, rw=self.rw)
+        return self.out
+
+
+class CoopRunnerCapacity:
+    """Bounded-capacity runner with the ownership rules of CoopRunner3072
+    (runtime/ds41/moe_coop3072.py:261-402). Subclasses fix the default capacity."""
+
+    DEFAULT_MAX_ROWS = 512
+
+    def __init__(self, device="cuda", topk=6, hidden=5120, inter=2304, max_rows=None, *, n_local=None,
+                 verbose=False):
+        max_rows = self.DEFAULT_MAX_ROWS if max_rows is None else max_rows
+        if type(topk) is not int or not 1 <= topk <= 32:
+            raise ValueError("topk must be an integer in 1..32")
+        if type(max_rows) is not int or not 1 <= max_rows <= 65536 // topk:
+            raise ValueError("max_rows out of range")
+        if hidden % 128 or inter % 128 or hidden < 128 or inter < 128:
+            raise ValueError("hidden and inter must be positive multiples of 128")
+        if not torch.cuda.is_available():
+            raise RuntimeError("the MoE runner requires a GPU; there is no CPU numerical fallback")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("the MoE runner requires a GPU device")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        with torch.cuda.device(self.device):
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("runner construction during capture is unsupported")
+        self.topk, self.hidden, self.inter, self.max_rows = topk, hidden, inter, max_rows
+        self.n_local = n_local
+        self.verbose = verbose
+        self._stream = torch.cuda.current_stream(self.device)
+        self._owner_stream = self._stream.cuda_stream
+        self._owner_thread = threading.get_ident()
+        self._lock, self._failed = threading.Lock(), False
+        self._closed, self._close_drains = False, 0
+        self._failed_inputs = []
+        self._table_valid = False
+        self._ws = {}
+        self._last_ws = None
+        self.out = torch.empty(max_rows, hidden, device=self.device, dtype=torch.float32)
+        self.rw = torch.empty(max_rows, topk, device=self.device, dtype=torch.float16)
+        self.table = torch.zeros(2 + 2 * max_rows * topk + 1, device=self.device, dtype=torch.int32)
+        self._prep_ws = torch.zeros(ops.prepare_routes_workspace_bytes(max_rows, topk), device=self.device,
+                                    dtype=torch.uint8)
+
+    # -- helpers -------------------------------------------------------------------------------
+
+    def _workspace(self, n_local):
+        ws = self._ws.get(n_local)
+        if ws is None:
+            ws = ops.MoeWorkspace(self.device, rows_max=self.max_rows, hidden=self.hidden, inter=self.inter,
+                                  topk=self.topk, n_local=n_local, has_shared=False)
+            self._ws[n_local] = ws
+        return ws
+
+    def _enter(self, what, allow_capture=False):
+        if threading.get_ident() != self._owner_thread:
+            raise RuntimeError(f"{what} requires the runner's owner thread")
+        if self._failed or self._closed:
+            raise RuntimeError("runner failed or closed; discard it")
+        if torch.cuda.current_stream(self.device).cuda_stream != self._owner_stream:
+            raise RuntimeError(f"{what} requires the construction stream; no implicit cross-stream reuse")
+        if not allow_capture:
+            with torch.cuda.device(self.device):
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError(f"{what} cannot be captured (it synchronises with the host)")
+        if not self._lock.acquire(blocking=False):
+            raise RuntimeError("runner is already in use")
+
+    def _routes(self, x, sel, weights):
+        if (not isinstance(x, torch.Tensor) or x.ndim != 2 or x.shape[1] != self.hidden
+                or not 1 <= x.shape[0] <= self.max_rows or x.dtype not in (torch.float16, torch.bfloat16)):
+            raise ValueError(f"x must be Half/BF16 [1..{self.max_rows},{self.hidden}]")
+        rows = x.shape[0]
+        if (not isinstance(sel, torch.Tensor) or tuple(sel.shape) != (rows, self.topk) or sel.dtype != torch.int64
+                or not isinstance(weights, torch.Tensor) or weights.shape != sel.shape
+                or weights.dtype not in (torch.float16, torch.bfloat16, torch.float32)):
+            raise ValueError(f"routes/weights require [rows,{self.topk}] Long and Half/BF16/Float")
+        if any(t.device != self.device for t in (x, sel, weights)):
+            raise ValueError("inputs must be on the runner device")
+        return rows
+
+    # -- reference API ---------------------------------------------------------------------------
+
+    def run(self, x, sel, weights, packed, k, limit, *, check_bounds=True):
+        """Run M rows and return an OWNED fp32 ``[M, hidden]``. Pointer targets are leased by
+        the caller until the GPU is done with them."""
+        k = _check_rate(k)
+        limit = _check_limit(limit)
+        if check_bounds not in (True, False):
+            raise ValueError("check_bounds must be a bool")
+        rows = self._routes(x, sel, weights)
+        table = _pointer_table(packed, self.device, self.n_local)
+        self._enter("run", allow_capture=not check_bounds)
+        try:
+            stream = torch.cuda.current_stream(self.device)
+            x, sel = x.contiguous(), sel.contiguous()
+            ws = self._workspace(table.shape[1])
+            inputs = [x, sel, weights, table, ws.buffer, self.out, self.rw]
+            self._failed_inputs = inputs
+            for t in inputs:
+                t.record_stream(stream)
+            rw = self.rw[:rows]
+            rw.copy_(weights.to(torch.float16))
+            ws.clear_flags()
+            out = self.out[:rows]
+            ops.moe_forward(ws, x, table, out, limit=limit, bits=k, sel=sel, rw=rw)
+            self._last_ws = ws
+            self._table_valid = True
+            if check_bounds and int(ws.flags()[0].item()) != 0:
+                raise RuntimeError("expert index outside the pointer table")
+            output = out.clone()
+            self._failed_inputs = []
+            return output
+        except BaseException:
+            self._failed = True
+            raise
+        finally:
+            self._lock.release()
+
+    def prepare_routes(self, sel, weights, n_local):
+        """The run table of these routes (owned int32 ``[2 + 2*max_rows*topk + 1]``)."""
+        if type(n_local) is not int or not 1 <= n_local <= 512:
+            raise ValueError("n_local must be an integer in 1..512")
+        if (not isinstance(sel, torch.Tensor) or sel.dtype != torch.int64 or sel.ndim != 2
+                or not 1 <= sel.shape[0] <= self.max_rows or sel.shape[1] != self.topk
+                or not isinstance(weights, torch.Tensor) or weights.shape != sel.shape
+                or weights.dtype not in (torch.float16, torch.bfloat16, torch.float32)
+                or sel.device != self.device or weights.device != self.device):
+            raise ValueError("prepare requires same-device bounded Long routes and floating weights")
+        self._enter("prepare_routes")
+        try:
+            stream = torch.cuda.current_stream(self.device)
+            sel = sel.contiguous()
+            rw = self.rw[:len(sel)]
+            inputs = [sel, weights, self.rw, self.table, self._prep_ws]
+            self._failed_inputs = inputs
+            for t in inputs:
+                t.record_stream(stream)
+            rw.copy_(weights.to(torch.float16))
+            self._prep_ws[:4].zero_()
+            ops.prepare_routes(sel, rw, self.max_rows, n_local, runs=self.table, workspace=self._prep_ws)
+            self._last_ws = None
+            self._table_valid = True
+            output = self.table.clone()
+            self._failed_inputs = []
+            return output
+        except BaseException:
+            self._failed = True
+            raise
+        finally:
+            self._lock.release()
+
+    def run_table(self):
+        """Owned snapshot of the last run's (or prepare's) table."""
+        if not self._table_valid:
+            raise RuntimeError("no table yet")
+        self._enter("run_table")
+        try:
+            return (self._last_ws.runs() if self._last_ws is not None else self.table).clone()
+        except BaseException:
+            self._failed = True
+            raise
+        finally:
+            self._lock.release()
+
+    def lifecycle(self):
+        """Python ownership state (no device query)."""
+        return dict(failed=self._failed, closed=self._closed, close_drains=self._close_drains,
+                    owner_thread_matches=threading.get_ident() == self._owner_thread,
+                    failed_input_leases=len(self._failed_inputs), workspace_owners_retained=True,
+                    caller_weight_pointer_lease_required=True, raw_addresses_disclosed=False)
+
+    def close(self):
+        """Drain the construction stream; a failed drain keeps every lease."""
+        if threading.get_ident() != self._owner_thread:
+            raise RuntimeError("close requires the owner thread")
+        if self._closed:
+            return
+        if not self._lock.acquire(blocking=False):
+            raise RuntimeError("close while the runner is active")
+        try:
+            try:
+                self._stream.synchronize()
+            except BaseException:
+                self._failed = True
+                raise
+            self._close_drains += 1
+            self._failed_inputs = []
+            self._closed = True
+        finally:
+            self._lock.release()
+
+
+class CoopRunner512(CoopRunnerCapacity):
+    """runtime/ds41/moe_coop512.py:170 (default capacity 64 rows)."""
+    DEFAULT_MAX_ROWS = 64
+
+
+class CoopRunner2048(CoopRunnerCapacity):
+    """runtime/ds41/moe_coop2048.py:220 (default capacity 256 rows)."""
+    DEFAULT_MAX_ROWS = 256
+
+
+class CoopRunner3072(CoopRunnerCapacity):
+    """runtime/ds41/moe_coop3072.py:261 (default capacity 512 rows)."""
+    DEFAULT_MAX_ROWS = 512

@@ -41,30 +41,27 @@ static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
     size_t flags, meta, local, order, runs, chunks, rw16, xr, xsum, act, actsum, part_gu, part_d, total;
-    int slots_max, nslot_max, max_chunks, ks_gu, ks_d;
+    int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
 };
 
-static int default_ksplit(int work_items, int kt_n, int target)
-{
-    int ks = (target + work_items - 1) / work_items;
-    const int cap = kt_n / 8 < 16 ? kt_n / 8 : 16;
-    if (ks > cap) ks = cap;
-    if (ks < 1) ks = 1;
-    return ks;
-}
+// Rows of GEMV partials a workspace holds when the k-split is chosen on the device: enough
+// for the splits that fill the grid at small batches (ks * rows <= this), and one split of
+// every row of a full batch.
+constexpr int EVAMX_AUTO_PART_ROWS = 1024;
 
-// Down-GEMV k-splits cover whole 128-element chunks of I.
-static int down_ksplit(int requested, int work_items, int inter)
+// Waves the GEMV kernels keep resident: 4 per SIMD (their register budget) on every CU.
+static int gemv_waves()
 {
-    const int na = inter / 128;
-    int ks = requested;
-    if (ks <= 0) {
-        ks = (4096 + work_items - 1) / work_items;
-        if (ks > 16) ks = 16;
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus * 4 * 4;
     }
-    if (ks > na) ks = na;
-    if (ks < 1) ks = 1;
-    return ks;
+    return cached[dev];
 }
 
 static bool shape_ok(const evamx_moe_shape* s)
@@ -95,10 +92,13 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.nslot_max = L.slots_max + (s->has_shared ? s->rows_max : 0);
     const int routed_chunks = (L.slots_max < s->n_local ? L.slots_max : s->n_local) + L.slots_max / EVAMX_CHUNK;
     L.max_chunks = routed_chunks + (s->has_shared ? (s->rows_max + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
-    const int chunks_est = (L.slots_max < s->n_local ? L.slots_max : s->n_local) + (s->has_shared ? 1 : 0);
-    L.ks_gu = s->ksplit_gu ? s->ksplit_gu : default_ksplit(chunks_est * 2 * (s->inter / 128), s->hidden / 16, 4096);
-    if (L.ks_gu > s->hidden / 128) L.ks_gu = s->hidden / 128;
-    L.ks_d = down_ksplit(s->ksplit_down, chunks_est * (s->hidden / 128), s->inter);
+    L.ks_gu_max = s->hidden / 128 < 32 ? s->hidden / 128 : 32;
+    L.ks_d_max = s->inter / 128 < 32 ? s->inter / 128 : 32;
+    L.ks_gu = s->ksplit_gu > L.ks_gu_max ? L.ks_gu_max : s->ksplit_gu;
+    L.ks_d = s->ksplit_down > L.ks_d_max ? L.ks_d_max : s->ksplit_down;
+    const int auto_rows = L.nslot_max > EVAMX_AUTO_PART_ROWS ? L.nslot_max : EVAMX_AUTO_PART_ROWS;
+    L.cap_rows_gu = L.ks_gu ? L.ks_gu * L.nslot_max : auto_rows;
+    L.cap_rows_d = L.ks_d ? L.ks_d * L.nslot_max : auto_rows;
     size_t o = 0;
     L.flags = o;   o = al256(o + 64 * 4);
     L.meta = o;    o = al256(o + 64 * 4);
@@ -111,8 +111,8 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.xsum = o;    o = al256(o + (size_t)2 * L.nslot_max * (s->hidden / 128) * 4);
     L.act = o;     o = al256(o + (size_t)L.nslot_max * s->inter * 2);
     L.actsum = o;  o = al256(o + (size_t)L.nslot_max * (s->inter / 128) * 4);
-    L.part_gu = o; o = al256(o + (size_t)L.ks_gu * 2 * L.nslot_max * s->inter * 4);
-    L.part_d = o;  o = al256(o + (size_t)L.ks_d * L.nslot_max * s->hidden * 4);
+    L.part_gu = o; o = al256(o + (size_t)L.cap_rows_gu * 2 * s->inter * 4);
+    L.part_d = o;  o = al256(o + (size_t)L.cap_rows_d * s->hidden * 4);
     L.total = o;
     return L;
 }
@@ -356,6 +356,9 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.part_d = (float*)(ws + L.part_d);
     p.nslot_max = L.nslot_max;
     p.ks_gu = L.ks_gu; p.ks_d = L.ks_d;
+    p.ks_gu_max = L.ks_gu_max; p.ks_d_max = L.ks_d_max;
+    p.cap_rows_gu = L.cap_rows_gu; p.cap_rows_d = L.cap_rows_d;
+    p.gemv_waves = gemv_waves();
     p.out = a->out; p.out_stride = a->out_stride;
     moe_launch(p, (hipStream_t)stream, a->events);
     return launched("moe_forward");

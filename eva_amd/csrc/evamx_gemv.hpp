@@ -1,5 +1,4 @@
-// Wave-level decode GEMV, Hadamard and completion-counter helpers shared by the MoE and the
-// single-linear kernels.
+// Wave-level decode GEMV and Hadamard helpers shared by the MoE and the single-linear kernels.
 //
 // GEMV lane layout (wave64): lane = 8*i + q streams tile (kt, 8*cg + i) words q*K..q*K+K-1 with
 // one vector load per k-slice and owns output columns 16i+q and 16i+q+8 of the 128-column group
@@ -45,21 +44,30 @@ typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
 typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 
-// A lane's K words with one non-temporal 64/96/128-bit load (+1 dword at K=5).
+// Global-address-space view of a pointer. Loads through a generic pointer become flat loads,
+// which also count against the LDS/scalar counter: every wait for a scalar activation load
+// would then drain the whole weight prefetch ring.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const void* p)
+{
+    return (const __attribute__((address_space(1))) T*)p;
+}
+
+// A lane's K words with one non-temporal 64/96/128-bit global load (+1 dword at K=5).
 template <int K>
 __device__ __forceinline__ void load_words(LaneWords<K>& w, const uint32_t* p)
 {
     if constexpr (K == 2) {
-        const u32x2a v = __builtin_nontemporal_load((const u32x2a*)p);
+        const u32x2a v = __builtin_nontemporal_load(gptr<u32x2a>(p));
         w.b[1] = v.x; w.b[2] = v.y;
     } else if constexpr (K == 3) {
-        const u32x3a v = __builtin_nontemporal_load((const u32x3a*)p);
+        const u32x3a v = __builtin_nontemporal_load(gptr<u32x3a>(p));
         w.b[1] = v.x; w.b[2] = v.y; w.b[3] = v.z;
     } else {
-        const u32x4a v = __builtin_nontemporal_load((const u32x4a*)p);
+        const u32x4a v = __builtin_nontemporal_load(gptr<u32x4a>(p));
         w.b[1] = v.x; w.b[2] = v.y; w.b[3] = v.z; w.b[4] = v.w;
 #pragma unroll
-        for (int i = 4; i < K; ++i) w.b[i + 1] = __builtin_nontemporal_load(p + i);
+        for (int i = 4; i < K; ++i) w.b[i + 1] = __builtin_nontemporal_load(gptr<uint32_t>(p + i));
     }
 }
 
@@ -92,7 +100,7 @@ __device__ __forceinline__ uint32_t prev_word(uint32_t v, int lane)
 // Weight prefetch depth (k-slices in flight per wave): deeper for narrow chunks, whose loop
 // body is short; wide chunks keep register pressure in check.
 template <int TM>
-constexpr int prefetch_depth() { return TM <= 2 ? 8 : 4; }
+constexpr int prefetch_depth() { return TM <= 2 ? 7 : 4; }
 
 template <int K, int TM>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
@@ -115,10 +123,28 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
 #pragma unroll
     for (int d = 0; d < PF; ++d) load_words<K>(ring[d], bp + (size_t)min(kt0 + d, last) * slice);
 
-    auto step = [&](int kt, LaneWords<K>& slot) {
-        LaneWords<K> w = slot;
-        const int pre = __builtin_amdgcn_readfirstlane(min(kt + PF, last));
-        load_words<K>(slot, bp + (size_t)pre * slice);
+    // Narrow chunks load the next slice's activations (wave-uniform, scalar loads) one step
+    // ahead, so their latency hides behind a decode instead of stalling every step.
+    constexpr bool XPF = TM <= 2;
+    half2_t xa[TM][8];
+    auto load_x = [&](half2_t (&dst)[TM][8], int kt) {
+#pragma unroll
+        for (int m = 0; m < TM; ++m) {
+            if (m < tm) {
+                const half2_t* xp = (const half2_t*)src.A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dst[m][i] = xp[i];
+            }
+        }
+    };
+    if constexpr (XPF) load_x(xa, kt0);
+
+    // Decode the slot, then refill the same registers with the slice PF ahead (issuing the load
+    // before the decode would keep two copies of the slot live and make the compiler rotate
+    // registers through moves that wait for every load in flight), then the dot products.
+    auto step = [&](int kt, LaneWords<K>& w) {
+        half2_t xn[TM][8];
+        if constexpr (XPF) load_x(xn, min(kt + 1, last));
         w.b[0] = prev_word(w.b[K], lane);
         half2_t wp[16];
 #define EVAMX_DEC_UNIT(U)                                \
@@ -131,24 +157,36 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
         EVAMX_DEC_UNIT(2)
         EVAMX_DEC_UNIT(3)
 #undef EVAMX_DEC_UNIT
+        const int pre = __builtin_amdgcn_readfirstlane(min(kt + PF, last));
+        load_words<K>(w, bp + (size_t)pre * slice);
 #pragma unroll
         for (int m = 0; m < TM; ++m) {
             if (m < tm) {
-                const half2_t* xp = (const half2_t*)src.A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
-                half2_t xa[8];
+                if constexpr (!XPF) {
+                    const half2_t* xp = (const half2_t*)src.A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xa[i] = xp[i];
+                    for (int i = 0; i < 8; ++i) xa[m][i] = xp[i];
+                }
                 float a0 = acc[m][0], a1 = acc[m][1];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    a0 = dot2(wp[4 * u + 0], xa[u], a0);
-                    a0 = dot2(wp[4 * u + 1], xa[u + 4], a0);
-                    a1 = dot2(wp[4 * u + 2], xa[u], a1);
-                    a1 = dot2(wp[4 * u + 3], xa[u + 4], a1);
+                    a0 = dot2(wp[4 * u + 0], xa[m][u], a0);
+                    a0 = dot2(wp[4 * u + 1], xa[m][u + 4], a0);
+                    a1 = dot2(wp[4 * u + 2], xa[m][u], a1);
+                    a1 = dot2(wp[4 * u + 3], xa[m][u + 4], a1);
                 }
                 acc[m][0] = a0;
                 acc[m][1] = a1;
             }
+            // wide chunks: keep at most four tokens' activations (32 SGPRs) live at a time
+            if constexpr (TM >= 8)
+                if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (XPF) {
+#pragma unroll
+            for (int m = 0; m < TM; ++m)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xa[m][i] = xn[m][i];
         }
         // keep the next step's scalar activation loads out of this one (register pressure)
         __builtin_amdgcn_sched_barrier(0);
@@ -167,7 +205,10 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
 // GEMV for a chunk of tm rows over the 128-element k-chunks [c0, c1) with the smallest
 // template that fits; writes fp32 partials part[slot_of[m] * part_stride + column] =
 // sum_k x_k w_k = 0x1eee * sum_k x_k h_k + 0xc931 * sum_k x_k.
-template <int K>
+// Only the row variants up to TMAX are compiled in, so a launch for narrow chunks is not
+// register-allocated for the widest one. A chunk of more than TMAX rows (possible only when
+// given routes repeat an expert within a token) is processed TMAX rows at a time.
+template <int K, int TMAX>
 __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
                                            const GlobalRows& src, const int* slot_of, int tm, float* part,
                                            size_t part_stride)
@@ -178,13 +219,13 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
     {                                                                                           \
         uint32_t aoff[TMV];                                                                     \
         _Pragma("unroll") for (int m = 0; m < TMV; ++m)                                         \
-            aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tm ? slot_of[m] : slot_of[0]) * \
+            aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tr ? so[m] : so[0]) *        \
                                                                (int)(src.stride / 8));          \
         float acc[TMV][2];                                                                      \
-        gemv_wave<K, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, src, aoff, tm, acc);               \
+        gemv_wave<K, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, src, aoff, tr, acc);               \
         _Pragma("unroll") for (int m = 0; m < TMV; ++m) {                                       \
-            if (m < tm) {                                                                       \
-                const int row = slot_of[m];                                                     \
+            if (m < tr) {                                                                       \
+                const int row = so[m];                                                          \
                 const float* sp = src.sums + (size_t)row * src.sums_stride;                     \
                 float xs = 0.0f;                                                                \
                 for (int c = c0; c < c1; ++c) xs += sp[c];                                      \
@@ -194,27 +235,44 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
             }                                                                                   \
         }                                                                                       \
     }
-    if (tm <= 1) EVAMX_RUN(1)
-    else if (tm <= 2) EVAMX_RUN(2)
-    else if (tm <= 4) EVAMX_RUN(4)
-    else if (tm <= 8) EVAMX_RUN(8)
-    else EVAMX_RUN(16)
+    for (int r0 = 0; r0 < tm; r0 += TMAX) {
+        const int* so = slot_of + r0;
+        const int tr = tm - r0 < TMAX ? tm - r0 : TMAX;
+        if constexpr (TMAX == 1) EVAMX_RUN(1)
+        else if constexpr (TMAX == 2) {
+            if (tr <= 1) EVAMX_RUN(1)
+            else EVAMX_RUN(2)
+        } else if constexpr (TMAX == 4) {
+            if (tr <= 2) EVAMX_RUN(2)
+            else EVAMX_RUN(4)
+        } else {
+            static_assert(TMAX == 8, "row bounds are 1, 2, 4 or 8");
+            if (tr <= 1) EVAMX_RUN(1)
+            else if (tr <= 2) EVAMX_RUN(2)
+            else if (tr <= 4) EVAMX_RUN(4)
+            else EVAMX_RUN(8)
+        }
+    }
 #undef EVAMX_RUN
 }
 
 // Runtime rate (k2 = 2K) -> instantiated GEMV; integer rates 2..5.
+template <int TMAX>
 __device__ __forceinline__ void gemv_dispatch_k(int k2, const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
                                                 const GlobalRows& src, const int* slot_of, int tm, float* part,
                                                 size_t part_stride)
 {
     switch (k2) {
-        case 4: gemv_chunk<2>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 6: gemv_chunk<3>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 8: gemv_chunk<4>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 10: gemv_chunk<5>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 4: gemv_chunk<2, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 6: gemv_chunk<3, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 8: gemv_chunk<4, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 10: gemv_chunk<5, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
         default: break;
     }
 }
+
+// Smallest compiled row bound that covers `rows` rows per chunk (wider chunks loop over it).
+inline int tmax_for(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
 
 // Sum over the wave of one value per lane (order fixed by the butterfly).
 __device__ __forceinline__ float wave_sum(float v)

@@ -9,7 +9,7 @@ namespace evamx {
 
 constexpr int EVAMX_MAX_EXPERTS = 512;     // pointer-table entries per layer (reference: <= 384)
 constexpr int EVAMX_MAX_TOPK = 32;         // reference bound: top_k <= 32 (exl3_moe_coop_kernel.cuh:46)
-constexpr int EVAMX_CHUNK = 16;            // slots of one expert per GEMV work item
+constexpr int EVAMX_CHUNK = 8;             // slots of one expert per GEMV work item
 
 // Pointer-table rows, in the reference's order (ds41/cache.py:1877-1886).
 enum {
@@ -56,14 +56,42 @@ struct MoeParams {
     float* xsum;               // [2][nslot_max][H/128] their 128-chunk sums
     half_t* act;               // [nslot_max][I] rotated down inputs
     float* actsum;             // [nslot_max][I/128]
-    float* part_gu;            // [ks_gu][2][nslot_max][I]
-    float* part_d;             // [ks_d][nslot_max][H]
+    float* part_gu;            // [ks][2][nslot][I], nslot = rows of this call (moe_nslot)
+    float* part_d;             // [ks][nslot][H]
     int nslot_max;
-    int ks_gu, ks_d;
+    int ks_gu, ks_d;           // requested k-splits (0: chosen on the device, moe_ks)
+    int ks_gu_max, ks_d_max;   // bounds of the automatic choice
+    int cap_rows_gu, cap_rows_d;   // partial-buffer capacity in rows (ks * nslot <= cap)
+    int gemv_waves;            // grid of the GEMV kernels (waves resident on the device at once)
     // output
     float* out;
     int out_stride;
 };
+
+// Rows of the GEMV partial buffers in this call: the routed slots, then the shared expert's rows.
+__device__ __forceinline__ int moe_nslot(const MoeParams& p) { return p.T * p.topk + (p.has_shared ? p.T : 0); }
+
+// K-split of a GEMV with `units` (chunk, projection, 128 columns) work units: as many splits as
+// fill the resident grid once, within the bounds and the partial buffer. Every kernel that
+// reads the partials recomputes it from the same inputs.
+__device__ __forceinline__ int moe_ks(int req, int units, int waves, int kmax, int cap_rows, int nslot)
+{
+    if (req > 0) return req;
+    int ks = units > 0 ? waves / units : 1;
+    if (ks > kmax) ks = kmax;
+    if (ks > cap_rows / nslot) ks = cap_rows / nslot;
+    return ks < 1 ? 1 : ks;
+}
+
+__device__ __forceinline__ int ks_gate_up(const MoeParams& p, int nchunks)
+{
+    return moe_ks(p.ks_gu, nchunks * 2 * (p.I / 128), p.gemv_waves, p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
+}
+
+__device__ __forceinline__ int ks_down(const MoeParams& p, int nchunks)
+{
+    return moe_ks(p.ks_d, nchunks * (p.H / 128), p.gemv_waves, p.ks_d_max, p.cap_rows_d, moe_nslot(p));
+}
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);
 int moe_prepare_only(MoeParams& p, hipStream_t stream);

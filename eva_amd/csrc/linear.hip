@@ -46,6 +46,7 @@ __global__ __launch_bounds__(256) void lin_rotate_kernel(LinParams p)
     if (lane == 0) p.xsum[(size_t)r * nch + c] = sum;
 }
 
+template <int TMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void lin_gemv_kernel(LinParams p, const half_t* __restrict__ xr)
 {
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
     const int cg = wid / p.ks, ks = wid % p.ks;
     const int nch = p.in / 128;
     const int c0 = nch * ks / p.ks, c1 = nch * (ks + 1) / p.ks;
-    gemv_dispatch_k(p.k2, p.trellis, p.out / 16, cg, c0, c1, GlobalRows{xr, (size_t)p.in, p.xsum, nch}, k_iota,
+    gemv_dispatch_k<TMAX>(p.k2, p.trellis, p.out / 16, cg, c0, c1, GlobalRows{xr, (size_t)p.in, p.xsum, nch}, k_iota,
                     p.rows, p.part + (size_t)ks * p.rows * p.out, (size_t)p.out);
 }
 
@@ -126,7 +127,14 @@ int launch_linear(const void* x, int rows, int in, int out, const void* trellis,
     }
     {
         const int waves = (out / 128) * p.ks;
-        hipLaunchKernelGGL(lin_gemv_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.xr);
+        const dim3 grid((waves + 3) / 4);
+        const half_t* xr = p.xr;
+        switch (tmax_for(rows)) {
+            case 1: hipLaunchKernelGGL(lin_gemv_kernel<1>, grid, dim3(256), 0, stream, p, xr); break;
+            case 2: hipLaunchKernelGGL(lin_gemv_kernel<2>, grid, dim3(256), 0, stream, p, xr); break;
+            case 4: hipLaunchKernelGGL(lin_gemv_kernel<4>, grid, dim3(256), 0, stream, p, xr); break;
+            default: hipLaunchKernelGGL(lin_gemv_kernel<8>, grid, dim3(256), 0, stream, p, xr); break;
+        }
     }
     {
         const int waves = (out / 128) * rows;

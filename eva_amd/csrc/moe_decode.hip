@@ -32,19 +32,20 @@ namespace evamx {
 // for bit with the CPU restatement.
 
 #pragma clang fp contract(off)
+// exp by Cody-Waite range reduction (x = n ln2 + r, ln2 split in a 16-bit head and a tail so
+// that n * head is exact) and the degree-7 Taylor polynomial of e^r on |r| <= ln2/2.
 __device__ float exp_portable(float x)
 {
     x = fminf(fmaxf(x, -87.0f), 88.0f);
-    const float t = x * 1.4426950408889634f;
-    const float n = rintf(t);
-    const float r = t - n;
-    float p = 1.525273380405984e-05f;
-    p = p * r + 0.00015403530393381608f;
-    p = p * r + 0.0013333558146428443f;
-    p = p * r + 0.009618129107628477f;
-    p = p * r + 0.05550410866482158f;
-    p = p * r + 0.2402265069591007f;
-    p = p * r + 0.6931471805599453f;
+    const float n = rintf(x * 1.4426950408889634f);
+    const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187e-06f;
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
     p = p * r + 1.0f;
     return ldexpf(p, (int)n);
 }
@@ -344,17 +345,18 @@ __device__ void rotate_item(const MoeParams& p, int s, int e, int c, int proj, i
 }
 
 // ---------------------------------------------------------------------------------------------
-// Prepare for small batches (T*topk <= EVAMX_SMALL_SLOTS, T <= EVAMX_CHUNK): every workgroup
-// routes and groups in LDS, workgroup 0 publishes, then all workgroups rotate.
+// Prepare for small batches (T*topk <= EVAMX_SMALL_SLOTS, T <= EVAMX_SMALL_ROWS): every
+// workgroup routes and groups in LDS, workgroup 0 publishes, then all workgroups rotate.
 
 constexpr int EVAMX_SMALL_SLOTS = 512;
+constexpr int EVAMX_SMALL_ROWS = 16;
 
 struct SmallLds {
     ExpertLds ex;
     int sel[EVAMX_SMALL_SLOTS];
     half_t rw[EVAMX_SMALL_SLOTS];
     int local[EVAMX_SMALL_SLOTS];
-    int order[EVAMX_SMALL_SLOTS + EVAMX_CHUNK];
+    int order[EVAMX_SMALL_SLOTS + EVAMX_SMALL_ROWS];
 };
 
 __global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
@@ -468,33 +470,41 @@ __device__ __forceinline__ const void* expert_ptr(const MoeParams& p, int e, int
     return (const void*)p.tables[(size_t)row * p.tbl_stride + e];
 }
 
-// Gate/up GEMV: per wave (chunk, 128 columns, gate|up, k-split) -> part_gu[ks][proj][slot][I].
+// Gate/up GEMV: one wave per work item (chunk, 128 columns, gate|up, k-split) ->
+// part_gu[ks][proj][slot][I].
+template <int TMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_kernel(MoeParams p, const half_t* __restrict__ xr)
 {
-    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int wid0 = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nchunks = __builtin_amdgcn_readfirstlane(p.meta[0]);
     const int ncg = p.I / 128;
-    const int S = p.ks_gu;
-    const int c = wid / (2 * ncg * S);
-    if (c >= p.meta[0]) return;
-    int rem = wid % (2 * ncg * S);
-    const int cg = rem / (2 * S);
-    rem %= 2 * S;
-    const int proj = rem / S, ks = rem % S;
-
-    const int* ch = p.chunks + 4 * c;
-    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-    const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
-    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
-    const int* slot_of = p.order + begin;
-
+    const int S = ks_gate_up(p, nchunks);
+    const int nslot = moe_nslot(p);
     const int nch = p.H / 128;
-    const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
-    const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, proj == 0 ? EVAMX_TBL_G_TRELLIS : EVAMX_TBL_U_TRELLIS);
-    const GlobalRows src{xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch,
-                         nch};
-    float* part = p.part_gu + ((size_t)ks * 2 + proj) * p.nslot_max * p.I;
-    gemv_dispatch_k(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
+    // one item per wave: the launch covers max(gemv_waves, max_chunks * 2 * ncg) >= items
+    const int wid = wid0;
+    if (wid >= nchunks * 2 * ncg * S) return;
+    {
+        const int c = wid / (2 * ncg * S);
+        int rem = wid % (2 * ncg * S);
+        const int cg = rem / (2 * S);
+        rem %= 2 * S;
+        const int proj = rem / S, ks = rem % S;
+
+        const int* ch = p.chunks + 4 * c;
+        const int e = __builtin_amdgcn_readfirstlane(ch[0]);
+        const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
+        const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
+        const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
+        const int* slot_of = p.order + begin;
+
+        const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
+        const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, proj == 0 ? EVAMX_TBL_G_TRELLIS : EVAMX_TBL_U_TRELLIS);
+        const GlobalRows src{xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H,
+                             p.xsum + (size_t)proj * p.nslot_max * nch, nch};
+        float* part = p.part_gu + ((size_t)ks * 2 + proj) * nslot * p.I;
+        gemv_dispatch_k<TMAX>(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
+    }
 }
 
 // Activation epilogue: one wave per (grouped row o, 128-chunk a of I). Sums the gate/up
@@ -518,14 +528,15 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const half_t* u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
     const half_t* d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
     const float L = p.limit;
-    const int Sg = p.ks_gu;
+    const int Sg = ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[0]));
+    const int nslot = moe_nslot(p);
     float g[2], u[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int col = a * 128 + lane_col(lane, h);
         const float* pg = p.part_gu + (size_t)s * p.I + col;
-        const size_t pstride = (size_t)2 * p.nslot_max * p.I;        // next k-split
-        const size_t ustride = (size_t)p.nslot_max * p.I;            // gate -> up
+        const size_t pstride = (size_t)2 * nslot * p.I;              // next k-split
+        const size_t ustride = (size_t)nslot * p.I;                  // gate -> up
         float sg = 0.0f, su = 0.0f;
         int q = 0;
         for (; q + 4 <= Sg; q += 4) {
@@ -583,37 +594,44 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     if (lane == 0) p.actsum[(size_t)s * na + a] = sum;
 }
 
-// Down GEMV: per wave (chunk, 128 columns, k-split) -> part_d[ks][slot][H].
+// Down GEMV: one wave per work item (chunk, 128 columns, k-split) -> part_d[ks][slot][H].
+template <int TMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_down_kernel(MoeParams p, const half_t* __restrict__ act)
 {
-    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int wid0 = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nchunks = __builtin_amdgcn_readfirstlane(p.meta[0]);
     const int ncg = p.H / 128;
-    const int S = p.ks_d;
-    const int c = wid / (ncg * S);
-    if (c >= p.meta[0]) return;
-    const int rem = wid % (ncg * S);
-    const int cg = rem / S, ks = rem % S;
-
-    const int* ch = p.chunks + 4 * c;
-    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-    const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
-    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
-    const int* slot_of = p.order + begin;
-
+    const int S = ks_down(p, nchunks);
+    const int nslot = moe_nslot(p);
     const int na = p.I / 128;
-    const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
-    const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, EVAMX_TBL_D_TRELLIS);
-    float* part = p.part_d + (size_t)ks * p.nslot_max * p.H;
-    gemv_dispatch_k(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{act, (size_t)p.I, p.actsum, na}, slot_of, tm, part,
-                    (size_t)p.H);
+    // one item per wave: the launch covers max(gemv_waves, max_chunks * ncg) >= items
+    const int wid = wid0;
+    if (wid >= nchunks * ncg * S) return;
+    {
+        const int c = wid / (ncg * S);
+        const int rem = wid % (ncg * S);
+        const int cg = rem / S, ks = rem % S;
+
+        const int* ch = p.chunks + 4 * c;
+        const int e = __builtin_amdgcn_readfirstlane(ch[0]);
+        const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
+        const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
+        const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
+        const int* slot_of = p.order + begin;
+
+        const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
+        const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, EVAMX_TBL_D_TRELLIS);
+        float* part = p.part_d + (size_t)ks * nslot * p.H;
+        gemv_dispatch_k<TMAX>(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{act, (size_t)p.I, p.actsum, na}, slot_of,
+                              tm, part, (size_t)p.H);
+    }
 }
 
 // Sum of the down k-split partials of slot s on this lane's two columns, fixed order; loads of
 // four splits are issued before their adds.
 __device__ __forceinline__ void sum_partials(const MoeParams& p, int s, int cg, int lane, int S, float (&v)[2])
 {
-    const size_t stride = (size_t)p.nslot_max * p.H;
+    const size_t stride = (size_t)moe_nslot(p) * p.H;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const float* pp = p.part_d + (size_t)s * p.H + cg * 128 + lane_col(lane, h);
@@ -643,7 +661,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
     const int ncg = p.H / 128;
     const int row = blockIdx.x / ncg, cg = blockIdx.x % ncg;
     const int slots = p.T * p.topk;
-    const int S = p.ks_d;
+    const int S = ks_down(p, __builtin_amdgcn_readfirstlane(p.meta[0]));
     const int c0 = lane_col(lane, 0), c1 = lane_col(lane, 1);
     const int col0 = cg * 128 + c0, col1 = cg * 128 + c1;
     const int nitems = p.topk + (p.has_shared ? 1 : 0);
@@ -702,7 +720,7 @@ int moe_prepare_only(MoeParams& p, hipStream_t stream)
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T <= EVAMX_CHUNK; }
+bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T <= EVAMX_SMALL_ROWS; }
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
 {
@@ -721,20 +739,38 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         hipLaunchKernelGGL(moe_rotate_kernel, dim3(256), dim3(256), 0, stream, p);
     }
     mark(1);
+    // Chunks hold at most min(T, EVAMX_CHUNK) rows: each token picks an expert once, and the
+    // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
+    const int tmax = tmax_for(p.T < EVAMX_CHUNK ? p.T : EVAMX_CHUNK);
     {
-        const int waves = p.max_chunks * 2 * (p.I / 128) * p.ks_gu;
-        hipLaunchKernelGGL(moe_gate_up_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.xr);
+        const int units = p.max_chunks * 2 * (p.I / 128);
+        const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
+        const half_t* xr = p.xr;
+        switch (tmax) {
+            case 1: hipLaunchKernelGGL(moe_gate_up_kernel<1>, grid, dim3(256), 0, stream, p, xr); break;
+            case 2: hipLaunchKernelGGL(moe_gate_up_kernel<2>, grid, dim3(256), 0, stream, p, xr); break;
+            case 4: hipLaunchKernelGGL(moe_gate_up_kernel<4>, grid, dim3(256), 0, stream, p, xr); break;
+            default: hipLaunchKernelGGL(moe_gate_up_kernel<8>, grid, dim3(256), 0, stream, p, xr); break;
+        }
     }
     mark(2);
     {
         const int waves = nslot * (p.I / 128);
         hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
-        const int dwaves = p.max_chunks * (p.H / 128) * p.ks_d;
-        hipLaunchKernelGGL(moe_down_kernel, dim3((dwaves + 3) / 4), dim3(256), 0, stream, p, (const half_t*)p.act);
+        mark(3);
+        const int units = p.max_chunks * (p.H / 128);
+        const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
+        const half_t* act = p.act;
+        switch (tmax) {
+            case 1: hipLaunchKernelGGL(moe_down_kernel<1>, grid, dim3(256), 0, stream, p, act); break;
+            case 2: hipLaunchKernelGGL(moe_down_kernel<2>, grid, dim3(256), 0, stream, p, act); break;
+            case 4: hipLaunchKernelGGL(moe_down_kernel<4>, grid, dim3(256), 0, stream, p, act); break;
+            default: hipLaunchKernelGGL(moe_down_kernel<8>, grid, dim3(256), 0, stream, p, act); break;
+        }
     }
-    mark(3);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(256), 0, stream, p);
     mark(4);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(256), 0, stream, p);
+    mark(5);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -16,14 +16,17 @@ SCORE_FNS = {"sigmoid": _lib.SCORE_SIGMOID, "sqrt_softplus": _lib.SCORE_SQRT_SOF
 RATES = (2.0, 3.0, 4.0, 5.0)
 
 
-def _dev(t: torch.Tensor, name: str, dtype=None, ndim=None):
+def _dev(t: torch.Tensor, name: str, dtype=None, ndim=None, row_strided=False):
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor")
     if dtype is not None and t.dtype != dtype:
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
     if ndim is not None and t.ndim != ndim:
         raise ValueError(f"{name} must have {ndim} dims")
-    if not t.is_contiguous():
+    if row_strided:
+        if t.stride(-1) != 1 or (t.ndim == 2 and t.stride(0) < t.shape[1]):
+            raise ValueError(f"{name} must have unit column stride and non-overlapping rows")
+    elif not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
     return t
 
@@ -58,9 +61,13 @@ def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: 
         raise ValueError("x / trellis / suh / svh shapes disagree")
     if out is None:
         out = torch.empty(m, n_out, dtype=torch.float16, device=x.device)
+    _dev(out, "out", torch.float16, 2)
+    if tuple(out.shape) != (m, n_out):
+        raise ValueError(f"out must be [{m}, {n_out}]")
     need = lib().evamx_exl3_linear_workspace_bytes(m, n_in, n_out)
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _dev(workspace, "workspace", torch.uint8, 1)
     check(lib().evamx_exl3_linear(ptr(x), m, n_in, n_out, ptr(trellis), ptr(suh), ptr(svh), float(bits), ptr(out),
                                   ptr(workspace), workspace.numel(), stream_handle(x.device)), "evamx_exl3_linear")
     return out
@@ -79,6 +86,13 @@ def route_topk(logits: torch.Tensor, topk: int, score_fn: str = "sigmoid", sel_b
     check(lib().evamx_route_topk(ptr(logits), ptr(sel_bias), t, e, topk, SCORE_FNS[score_fn], float(route_scale),
                                  ptr(idx), ptr(w), ptr(rw), stream_handle(logits.device)), "evamx_route_topk")
     return idx, w, rw
+
+
+def prepare_routes_workspace_bytes(capacity: int, topk: int) -> int:
+    n = lib().evamx_prepare_routes_workspace_bytes(capacity, topk)
+    if n == 0:
+        raise ValueError("invalid capacity/topk")
+    return n
 
 
 def prepare_routes(sel: torch.Tensor, rw: torch.Tensor, capacity: int, n_local: int,
@@ -113,6 +127,11 @@ class MoeWorkspace:
         check(lib().evamx_moe_workspace_init(ctypes.byref(self.shape), ptr(self.buffer), stream_handle(self.device)),
               "evamx_moe_workspace_init")
 
+    def clear_flags(self) -> None:
+        """Zero the sticky device flag word (a fill kernel on the current stream)."""
+        check(lib().evamx_moe_workspace_init(ctypes.byref(self.shape), ptr(self.buffer), stream_handle(self.device)),
+              "evamx_moe_workspace_init")
+
     def runs(self) -> torch.Tensor:
         """View of the run table written by the last forward."""
         slots = self.shape.rows_max * self.shape.topk
@@ -139,14 +158,14 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
     must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
     the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
-    ``events``: optional ctypes array of 5 hipEvent_t handles recorded around the launches.
+    ``events``: optional ctypes array of 6 hipEvent_t handles recorded around the 5 stages.
     """
     s = ws.shape
-    _dev(x, "x", None, 2)
+    _dev(x, "x", None, 2, row_strided=True)
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("x must be fp16 or bf16")
     _dev(tables, "tables", torch.int64, 2)
-    _dev(out, "out", torch.float32, 2)
+    _dev(out, "out", torch.float32, 2, row_strided=True)
     if tables.shape != (9, s.n_local):
         raise ValueError(f"tables must be [9, {s.n_local}]")
     rows = x.shape[0]

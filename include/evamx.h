@@ -97,8 +97,9 @@ typedef struct evamx_moe_shape {
     int32_t topk;         /* <= 32 */
     int32_t n_local;      /* pointer-table entries, <= 512 */
     int32_t has_shared;   /* 1: a shared expert is added to every row */
-    int32_t ksplit_gu;    /* k-splits of the gate/up GEMV (0: default for the shape) */
-    int32_t ksplit_down;  /* k-splits of the down GEMV (0: default for the shape) */
+    int32_t ksplit_gu;    /* k-splits of the gate/up GEMV (0: chosen per call on the device
+                             from the number of expert chunks, to fill the GPU once) */
+    int32_t ksplit_down;  /* k-splits of the down GEMV (0: likewise) */
 } evamx_moe_shape;
 
 typedef struct evamx_moe_args {
@@ -132,8 +133,9 @@ typedef struct evamx_moe_args {
     int32_t out_stride;           /* elements; >= hidden */
     void* workspace;              /* device, evamx_moe_workspace_bytes(&shape) bytes */
     size_t workspace_bytes;
-    /* optional: 5 hipEvent_t recorded before each of the 4 launches and after the last
-     * (per-launch timing on the launch stream); NULL for none */
+    /* optional: 6 hipEvent_t recorded on the launch stream around the 5 stages (prepare,
+     * gate/up GEMV, activation, down GEMV, combine): events[i] before stage i, events[5]
+     * after the last; NULL for none */
     void* const* events;
 } evamx_moe_args;
 

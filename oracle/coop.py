@@ -30,6 +30,8 @@ float64 formula built from ``scipy.linalg.hadamard`` and plain matrix products.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from . import exl3
@@ -43,17 +45,16 @@ F32 = np.float32
 # for operation by the HIP router so that scores and selection keys agree bit for bit.
 
 _LOG2E = F32(1.4426950408889634)
-_EXP_COEF = [F32(c) for c in (1.0, 0.6931471805599453, 0.2402265069591007, 0.05550410866482158,
-                               0.009618129107628477, 0.0013333558146428443, 0.00015403530393381608,
-                               1.525273380405984e-05)]
+_LN2_HI = F32(0.693145751953125)          # 16 significant bits: n * _LN2_HI is exact for |n| < 256
+_LN2_LO = F32(1.428606765330187e-06)
+_EXP_COEF = [F32(1.0 / math.factorial(i)) for i in range(8)]
 
 
 def exp_f32(x):
-    """2^(x log2 e) with round-half-even range reduction and a degree-7 Taylor polynomial."""
+    """e^x by Cody-Waite reduction x = n ln2 + r and the degree-7 Taylor polynomial of e^r."""
     x = np.clip(np.asarray(x, dtype=F32), F32(-87.0), F32(88.0))
-    t = (x * _LOG2E).astype(F32)
-    n = np.rint(t).astype(F32)
-    r = (t - n).astype(F32)
+    n = np.rint((x * _LOG2E).astype(F32)).astype(F32)
+    r = ((x - (n * _LN2_HI).astype(F32)).astype(F32) - (n * _LN2_LO).astype(F32)).astype(F32)
     p = _EXP_COEF[7]
     for c in _EXP_COEF[6::-1]:
         p = (p * r).astype(F32)

@@ -1,0 +1,226 @@
+"""Pins the routing / grouping / expert-math oracle (``oracle/coop.py``) independently.
+
+- router: brute-force sort with the stable key of ``_stable_topk_indices``
+  (runtime/ds41/model.py:940-953), the special cases T=1 and all-equal rows, +0 == -0, and the
+  portable fp32 score functions against float64 math;
+- run table: invariants that characterise ``reference_runs``/``reference_table``
+  (runtime/ds41/moe_coop3072.py:64-106): a permutation of the active slots sorted by
+  (expert, slot), cuts exactly at expert changes and every 8 slots, run count
+  sum(ceil(n_e/8)); plus a hand-worked table;
+- expert / layer math: an independent dense float64 formula with the Sylvester matrix of
+  ``scipy.linalg.hadamard`` and plain matrix products, the activation semantics of
+  K.cuh:115-129 (clamp after SiLU) vs kernels.py:213-217 (clamp before SiLU), and exact
+  linearity in the routing weights.
+"""
+import math
+
+import numpy as np
+import pytest
+import scipy.linalg
+
+from oracle import coop, exl3, synth
+
+H128 = scipy.linalg.hadamard(128).astype(np.float64) / math.sqrt(128.0)
+
+
+# ---------------------------------------------------------------------------------------------
+# Router
+
+
+def test_stable_topk_brute_force_with_ties():
+    rng = np.random.default_rng(0)
+    keys = rng.integers(-3, 4, size=(50, 40)).astype(np.float32)       # many ties
+    keys[:, 7] = -0.0
+    keys[:, 9] = 0.0
+    got = coop.stable_topk(keys, 6)
+    for r in range(keys.shape[0]):
+        want = sorted(range(40), key=lambda i: (-float(keys[r, i]), i))[:6]
+        assert got[r].tolist() == want
+
+
+def test_router_special_cases():
+    z = np.zeros((1, 256), dtype=np.float32)
+    idx, w = coop.route(z, 8)
+    assert idx.tolist() == [list(range(8))]
+    assert np.allclose(w, 1.0 / 8, rtol=1e-6)
+    idx, w = coop.route(np.full((3, 64), 0.25, np.float32), 4, "sqrt_softplus", route_scale=1.5)
+    assert idx.tolist() == [[0, 1, 2, 3]] * 3
+    assert np.allclose(w.sum(-1), 1.5, rtol=1e-6)
+
+
+def test_router_selection_and_weights():
+    rng = np.random.default_rng(1)
+    z = rng.standard_normal((16, 256)).astype(np.float32)
+    bias = (rng.standard_normal(256) * 0.1).astype(np.float32)
+    for fn, f64 in (("sigmoid", lambda v: 1 / (1 + np.exp(-v))),
+                    ("sqrt_softplus", lambda v: np.sqrt(np.log1p(np.exp(v))))):
+        for b in (None, bias):
+            idx, w = coop.route(z, 8, fn, b, route_scale=2.5)
+            s64 = f64(z.astype(np.float64))
+            key = s64 + (0 if b is None else b.astype(np.float64))
+            want = np.argsort(-key, axis=-1, kind="stable")[:, :8]
+            assert np.array_equal(idx, want)
+            g = np.take_along_axis(s64, want, -1)
+            assert np.allclose(w, g / g.sum(-1, keepdims=True) * 2.5, rtol=2e-6)
+
+
+def test_portable_score_functions():
+    z = np.linspace(-30, 30, 20001, dtype=np.float32)
+    e = coop.exp_f32(z).astype(np.float64)
+    assert np.max(np.abs(e / np.exp(z.astype(np.float64)) - 1)) < 4e-7
+    s = coop.sigmoid_f32(z).astype(np.float64)
+    assert np.max(np.abs(s - 1 / (1 + np.exp(-z.astype(np.float64))))) < 2e-7
+    q = coop.sqrt_softplus_f32(z).astype(np.float64)
+    q64 = np.sqrt(np.logaddexp(0, z.astype(np.float64)))
+    assert np.max(np.abs(q / q64 - 1)) < 5e-7
+
+
+# ---------------------------------------------------------------------------------------------
+# Run table
+
+
+def _check_table(sel, rw, table, capacity, min_expert=-1, max_expert=0):
+    t, k = sel.shape
+    ok, local = coop.slot_active(sel, rw, min_expert, max_expert)
+    n_runs = int(table[0])
+    assert table[1] == 0
+    starts = table[2:2 + n_runs + 1]
+    n_active = int(ok.sum())
+    assert starts[0] == 0 and starts[-1] == n_active and np.all(np.diff(starts) > 0)
+    order = table[2 + capacity * k + 1:2 + capacity * k + 1 + n_active]
+    # a permutation of the active slots, sorted by (expert, slot)
+    act = np.nonzero(ok.reshape(-1))[0]
+    assert sorted(order.tolist()) == act.tolist()
+    keys = [(int(local.flat[s]), int(s)) for s in order]
+    assert keys == sorted(keys)
+    # cuts exactly at an expert change and every 8 slots of one expert
+    for a, b in zip(starts[:-1], starts[1:]):
+        es = {keys[i][0] for i in range(a, b)}
+        assert len(es) == 1 and b - a <= coop.ROWS
+    counts = np.bincount(local.reshape(-1)[act], minlength=1) if n_active else np.zeros(1, int)
+    assert n_runs == int(sum(-(-c // coop.ROWS) for c in counts if c))
+    # unused entries stay zero
+    assert not np.any(table[2 + n_runs + 1:2 + capacity * k + 1])
+    assert not np.any(table[2 + capacity * k + 1 + n_active:])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_run_table_invariants(seed):
+    rng = np.random.default_rng(seed)
+    t, k, E = int(rng.integers(1, 40)), int(rng.integers(1, 9)), int(rng.integers(2, 24))
+    sel = np.stack([rng.choice(E, size=k, replace=False) if k <= E else rng.integers(0, E, k) for _ in range(t)])
+    rw = rng.standard_normal((t, k)).astype(np.float16)
+    rw[rng.random((t, k)) < 0.2] = 0
+    cap = t + int(rng.integers(0, 4))
+    _check_table(sel, rw, coop.reference_table(sel, rw, cap), cap)
+    lo, hi = 1, max(2, E // 2)
+    _check_table(sel, rw, coop.reference_table(sel, rw, cap, lo, hi), cap, lo, hi)
+
+
+def test_run_table_hand_worked():
+    # 10 tokens all picking expert 3 in slot 0 and expert 1 in slot 1; slot 1 of token 4 inactive
+    sel = np.array([[3, 1]] * 10)
+    rw = np.ones((10, 2), np.float16)
+    rw[4, 1] = 0
+    table = coop.reference_table(sel, rw, capacity=10)
+    # expert 1: slots 1,3,5,7,11,13,15,17,19 (9 slots -> runs of 8 + 1); expert 3: 0,2,...,18 (8+2)
+    assert table[0] == 4
+    assert table[2:7].tolist() == [0, 8, 9, 17, 19]
+    order = table[23:23 + 19].tolist()
+    assert order == [1, 3, 5, 7, 11, 13, 15, 17, 19, 0, 2, 4, 6, 8, 10, 12, 14, 16, 18]
+    assert len(table) == 2 + 2 * 20 + 1
+
+
+def test_expert_csr_matches_runs():
+    rng = np.random.default_rng(7)
+    sel = rng.integers(0, 16, size=(20, 4))
+    rw = np.ones((20, 4), np.float16)
+    off, order = coop.expert_csr(sel, rw, 16)
+    flat = [s for _, ss in coop.reference_runs(sel, rw) for s in ss]
+    assert order.tolist() == flat
+    assert np.array_equal(np.diff(off), np.bincount(sel.reshape(-1), minlength=16))
+
+
+# ---------------------------------------------------------------------------------------------
+# Expert math
+
+
+def _dense_expert(x16, ew, limit, clamp_after=True):
+    """Float64 restatement with explicit matrices; fp16 rounding at the reference's points."""
+    f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
+    had = lambda a: (np.asarray(a, np.float64).reshape(-1, 128) @ H128).reshape(np.shape(a))
+    x = x16.astype(np.float64)
+    Wg, Wu, Wd = (ew.W(p).astype(np.float64) for p in "gud")
+    sv = lambda p, q: ew.parts[p][q].astype(np.float64)
+    g = had(f16(f16(had(x * sv("g", 1))) @ Wg)) * sv("g", 2)
+    u = had(f16(f16(had(x * sv("u", 1))) @ Wu)) * sv("u", 2)
+    silu = lambda v: v / (1 + np.exp(-v))
+    if clamp_after:
+        a = np.minimum(silu(g), limit) * np.clip(u, -limit, limit)
+    else:
+        a = silu(np.minimum(g, limit)) * np.clip(u, -limit, limit)
+    act = f16(had(a * sv("d", 1)))
+    return had(act @ Wd) * sv("d", 2)
+
+
+def _small_expert(rng, H=256, I=128, K=3):
+    return synth.expert(rng, H, I, K, svh_scale=1.0 / 16)
+
+
+def test_coop_expert_against_dense_formula():
+    rng = np.random.default_rng(11)
+    ew = _small_expert(rng)
+    x = (rng.standard_normal((3, 256)) * 2).astype(np.float16)
+    got = coop.coop_expert(x, ew, 10.0)
+    ref = _dense_expert(x, ew, 10.0)
+    assert coop.rel_err_rows(got, ref) < 5e-3
+
+
+def test_activation_clamp_semantics():
+    g = np.array([30.0, -30.0, 12.0, 0.5], np.float32)
+    u = np.array([20.0, 3.0, -15.0, 0.25], np.float32)
+    routed = coop.act_gate(g, u, 10.0)                  # min(silu(g), L) * clamp(u)
+    shared = coop.swiglu(g, u, 10.0)                    # silu(min(g, L)) * clamp(u)
+    silu = lambda v: v / (1 + math.exp(-v))
+    assert np.allclose(routed, [10 * 10, silu(-30) * 3, 10 * -10, silu(0.5) * 0.25], rtol=1e-6)
+    assert np.allclose(shared, [silu(10) * 10, silu(-30) * 3, silu(10) * -10, silu(0.5) * 0.25], rtol=1e-6)
+    assert routed[0] != shared[0]
+    assert np.array_equal(coop.act_gate(g, u, 0.0), (coop.silu_f32(g) * u).astype(np.float32))
+
+
+def test_moe_routed_linear_in_weights_and_sum_order():
+    rng = np.random.default_rng(12)
+    experts = [_small_expert(rng) for _ in range(4)]
+    x = rng.standard_normal((3, 256)).astype(np.float16)
+    sel = np.array([[0, 2], [1, 3], [2, 2]])
+    rw = np.array([[0.5, 0.25], [1.0, 0.0], [0.75, 0.125]], np.float16)
+    y = coop.moe_routed(x, sel, rw, experts, 10.0)
+    y2 = coop.moe_routed(x, sel, (rw * 2).astype(np.float16), experts, 10.0)
+    assert np.array_equal(y2, 2 * y)                    # power-of-two scaling is exact
+    o = {e: coop.coop_expert(x, experts[e], 10.0) for e in range(4)}
+    want = np.stack([0.5 * o[0][0] + 0.25 * o[2][0], 1.0 * o[1][1], 0.75 * o[2][2] + 0.125 * o[2][2]])
+    assert coop.rel_err_rows(y, want) < 1e-6
+    # EP filter: only local experts [1, 3) contribute, renumbered from 0
+    y_ep = coop.moe_routed(x, sel, rw, {0: experts[1], 1: experts[2]}, 10.0, min_expert=1, max_expert=3)
+    want_ep = np.stack([0.25 * o[2][0], 1.0 * o[1][1], 0.75 * o[2][2] + 0.125 * o[2][2]])
+    assert coop.rel_err_rows(y_ep, want_ep) < 1e-6
+
+
+def test_exl3_linear_and_shared_expert_against_dense():
+    rng = np.random.default_rng(13)
+    ew = _small_expert(rng, K=4)
+    x = rng.standard_normal((2, 256)).astype(np.float16)
+    tr, suh, svh = ew.parts["g"]
+    y = coop.exl3_linear(x, tr, suh, svh, 4)
+    had = lambda a: (np.asarray(a, np.float64).reshape(-1, 128) @ H128).reshape(np.shape(a))
+    ref = had(had(x.astype(np.float64) * suh.astype(np.float64)) @ ew.W("g").astype(np.float64)) * svh
+    assert coop.rel_err_rows(y, ref) < 5e-3
+    sh = coop.shared_expert(x, ew, 10.0)
+    ref_sh = _dense_expert(x, ew, 10.0, clamp_after=False)
+    assert coop.rel_err_rows(sh, ref_sh) < 1e-2
+
+
+def test_rel_err_rows_definition():
+    ref = np.array([[1.0, -4.0, 0.0], [0.0, 0.0, 2.0]])
+    y = ref + np.array([[0.04, 0.0, 0.0], [0.0, 0.01, 0.0]])
+    assert math.isclose(coop.rel_err_rows(y, ref), 0.01)
