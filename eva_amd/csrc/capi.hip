@@ -40,7 +40,8 @@ static bool gemv_rate(int k2) { return k2 == 4 || k2 == 6 || k2 == 8 || k2 == 10
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t flags, meta, local, order, runs, chunks, rw16, xr, xsum, act, actsum, part_gu, part_d, total;
+    size_t flags, meta, local, order, runs, chunks, unit_chunk, slot_mult, rw16, xr, xsum, act, actsum, part_gu, part_d,
+        total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
 };
 
@@ -105,7 +106,9 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.local = o;   o = al256(o + (size_t)L.slots_max * 4);
     L.order = o;   o = al256(o + (size_t)L.nslot_max * 4);
     L.runs = o;    o = al256(o + (size_t)(2 + 2 * L.slots_max + 1) * 4);
-    L.chunks = o;  o = al256(o + (size_t)L.max_chunks * 16);
+    L.chunks = o;  o = al256(o + (size_t)L.max_chunks * 32);
+    L.unit_chunk = o; o = al256(o + (size_t)EVAMX_MAX_MULT * L.max_chunks * 4);
+    L.slot_mult = o; o = al256(o + (size_t)L.nslot_max * 4);
     L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
     L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
     L.xsum = o;    o = al256(o + (size_t)2 * L.nslot_max * (s->hidden / 128) * 4);
@@ -347,6 +350,8 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.runs = (int*)(ws + L.runs);
     p.slots_max = L.slots_max;
     p.chunks = (int*)(ws + L.chunks);
+    p.unit_chunk = (int*)(ws + L.unit_chunk);
+    p.slot_mult = (int*)(ws + L.slot_mult);
     p.max_chunks = L.max_chunks;
     p.xr = (half_t*)(ws + L.xr);
     p.xsum = (float*)(ws + L.xsum);

@@ -49,9 +49,12 @@ struct MoeParams {
     int* order;                // [slots + T]
     int* runs;                 // reference run table [2 + 2*slots_max + 1]
     int slots_max;
-    int* chunks;               // [max_chunks][4]: expert (-1 shared), begin, count, k2
+    int* chunks;               // [max_chunks][8]: expert (-1 shared), begin, rows, k2, first unit,
+                               // units (cost weight of the chunk, chunk_mult), 0, 0
     int max_chunks;
-    int* meta;                 // [0] n_chunks, [1] n_active
+    int* unit_chunk;           // [EVAMX_MAX_MULT * max_chunks]: work unit -> chunk
+    int* slot_mult;            // [nslot_max]: cost weight of the chunk holding each slot/shared row
+    int* meta;                 // [0] n_chunks, [1] n_active, [2] n_units
     half_t* xr;                // [2][nslot_max][H] rotated gate/up inputs
     float* xsum;               // [2][nslot_max][H/128] their 128-chunk sums
     half_t* act;               // [nslot_max][I] rotated down inputs
@@ -71,26 +74,50 @@ struct MoeParams {
 // Rows of the GEMV partial buffers in this call: the routed slots, then the shared expert's rows.
 __device__ __forceinline__ int moe_nslot(const MoeParams& p) { return p.T * p.topk + (p.has_shared ? p.T : 0); }
 
-// K-split of a GEMV with `units` (chunk, projection, 128 columns) work units: as many splits as
-// fill the resident grid once, within the bounds and the partial buffer. Every kernel that
+// Cost weight of a chunk of `rows` rows: its decode is shared by the rows, each row adds its dot
+// products, so a chunk of 8 rows costs about three chunks of one. Work is handed out in units
+// of weight 1; a chunk of weight m gets m times the k-splits of a one-row chunk.
+constexpr int EVAMX_MAX_MULT = 3;
+__device__ __forceinline__ int chunk_mult(int rows) { return rows <= 3 ? 1 : rows <= 6 ? 2 : 3; }
+
+// K-split choice of a GEMV: `base` splits per work unit, as many as fill the resident grid once
+// (or the requested count), a chunk of weight m gets min(base * m, cap) splits (base when the
+// split is requested), and cap keeps ks * rows within the partial buffer. Every kernel that
 // reads the partials recomputes it from the same inputs.
-__device__ __forceinline__ int moe_ks(int req, int units, int waves, int kmax, int cap_rows, int nslot)
+struct KSplit {
+    int base, cap;
+};
+
+__device__ __forceinline__ KSplit moe_ksplit(int req, int items_per_split, int waves, int kmax, int cap_rows, int nslot)
 {
-    if (req > 0) return req;
-    int ks = units > 0 ? waves / units : 1;
-    if (ks > kmax) ks = kmax;
-    if (ks > cap_rows / nslot) ks = cap_rows / nslot;
-    return ks < 1 ? 1 : ks;
+    KSplit k;
+    k.cap = cap_rows / nslot < kmax ? cap_rows / nslot : kmax;
+    if (k.cap < 1) k.cap = 1;
+    if (req > 0) {
+        k.base = req;
+        k.cap = req;
+        return k;
+    }
+    int b = items_per_split > 0 ? waves / items_per_split : 1;
+    if (b > k.cap) b = k.cap;
+    k.base = b < 1 ? 1 : b;
+    return k;
 }
 
-__device__ __forceinline__ int ks_gate_up(const MoeParams& p, int nchunks)
+__device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
 {
-    return moe_ks(p.ks_gu, nchunks * 2 * (p.I / 128), p.gemv_waves, p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
+    const int v = k.base * mult;
+    return v < k.cap ? v : k.cap;
 }
 
-__device__ __forceinline__ int ks_down(const MoeParams& p, int nchunks)
+__device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
 {
-    return moe_ks(p.ks_d, nchunks * (p.H / 128), p.gemv_waves, p.ks_d_max, p.cap_rows_d, moe_nslot(p));
+    return moe_ksplit(p.ks_gu, units * 2 * (p.I / 128), p.gemv_waves, p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
+}
+
+__device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
+{
+    return moe_ksplit(p.ks_d, units * (p.H / 128), p.gemv_waves, p.ks_d_max, p.cap_rows_d, moe_nslot(p));
 }
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);

@@ -181,8 +181,16 @@ struct ExpertLds {
     int off[EVAMX_MAX_EXPERTS + 1];
     int run_base[EVAMX_MAX_EXPERTS + 1];
     int chunk_base[EVAMX_MAX_EXPERTS + 1];
+    int unit_base[EVAMX_MAX_EXPERTS + 1];
     int fill[EVAMX_MAX_EXPERTS];
 };
+
+// Work units (summed chunk weights) of an expert with n active slots.
+__device__ __forceinline__ int expert_units(int n)
+{
+    const int full = n / EVAMX_CHUNK, rest = n % EVAMX_CHUNK;
+    return full * chunk_mult(EVAMX_CHUNK) + (rest ? chunk_mult(rest) : 0);
+}
 
 // Exclusive scan of a[0..n) in place by one wave, a[n] = total (n <= 1024).
 __device__ void wave_excl_scan(int* a, int n, int lane)
@@ -245,10 +253,12 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
             ex.off[e] = ex.cnt[e];
             ex.run_base[e] = (ex.cnt[e] + 7) / 8;
             ex.chunk_base[e] = (ex.cnt[e] + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
+            ex.unit_base[e] = expert_units(ex.cnt[e]);
         }
         wave_excl_scan(ex.off, E, lane);
         wave_excl_scan(ex.run_base, E, lane);
         wave_excl_scan(ex.chunk_base, E, lane);
+        wave_excl_scan(ex.unit_base, E, lane);
         // Stable scatter by (expert, slot): blocks of 64 slots in order; lanes holding the same
         // expert find each other with one ballot per expert-index bit.
         for (int s0 = 0; s0 < slots; s0 += 64) {
@@ -281,31 +291,53 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
     __syncthreads();
 }
 
-// Chunks of <= EVAMX_CHUNK slots per expert, then the shared expert's rows.
-__device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, int* chunks)
+// Chunks of <= EVAMX_CHUNK slots per expert, then the shared expert's rows; their work units
+// (unit -> chunk map) and each slot's chunk weight. `order` is the grouped slot order.
+__device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int* order)
 {
     const int t = threadIdx.x, nt = blockDim.x;
     const int E = p.n_local;
     const int n_active = ex.off[E];
     for (int e = t; e < E; e += nt) {
         const int n = ex.cnt[e];
+        int u = ex.unit_base[e];
         for (int j = 0; j * EVAMX_CHUNK < n; ++j) {
-            int* c = chunks + 4 * (ex.chunk_base[e] + j);
+            const int ci = ex.chunk_base[e] + j;
+            const int rows = min(EVAMX_CHUNK, n - j * EVAMX_CHUNK);
+            const int m = chunk_mult(rows);
+            int* c = p.chunks + 8 * ci;
             c[0] = e;
             c[1] = ex.off[e] + j * EVAMX_CHUNK;
-            c[2] = min(EVAMX_CHUNK, n - j * EVAMX_CHUNK);
+            c[2] = rows;
             c[3] = p.k2_per_expert ? (int)p.k2_per_expert[e] : p.k2_uniform;
+            c[4] = u;
+            c[5] = m;
+            c[6] = 0;
+            c[7] = 0;
+            for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
+            for (int i = 0; i < rows; ++i) p.slot_mult[order[c[1] + i]] = m;
+            u += m;
         }
     }
     if (p.has_shared) {
         const int base = ex.chunk_base[E];
         const int nsc = (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
+        const int slots = p.T * p.topk;
         for (int j = t; j < nsc; j += nt) {
-            int* c = chunks + 4 * (base + j);
+            const int rows = min(EVAMX_CHUNK, p.T - j * EVAMX_CHUNK);
+            const int m = chunk_mult(rows);
+            const int u = ex.unit_base[E] + j * chunk_mult(EVAMX_CHUNK);     // earlier chunks are full
+            int* c = p.chunks + 8 * (base + j);
             c[0] = -1;
             c[1] = n_active + j * EVAMX_CHUNK;
-            c[2] = min(EVAMX_CHUNK, p.T - j * EVAMX_CHUNK);
+            c[2] = rows;
             c[3] = p.k2_shared;
+            c[4] = u;
+            c[5] = m;
+            c[6] = 0;
+            c[7] = 0;
+            for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
+            for (int i = 0; i < rows; ++i) p.slot_mult[slots + j * EVAMX_CHUNK + i] = m;
         }
     }
 }
@@ -313,6 +345,11 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, int* chunk
 __device__ __forceinline__ int total_chunks(const MoeParams& p, const ExpertLds& ex)
 {
     return ex.chunk_base[p.n_local] + (p.has_shared ? (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
+}
+
+__device__ __forceinline__ int total_units(const MoeParams& p, const ExpertLds& ex)
+{
+    return ex.unit_base[p.n_local] + (p.has_shared ? expert_units(p.T) : 0);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -389,13 +426,14 @@ __global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
     if (pub) {
         for (int s = t; s < slots; s += 256) p.local[s] = sh.local[s];
         for (int i = t; i < n_active + (p.has_shared ? p.T : 0); i += 256) p.order[i] = sh.order[i];
-        write_chunks(p, sh.ex, p.chunks);
+        write_chunks(p, sh.ex, sh.order);
         if (t == 0) {
             p.runs[0] = sh.ex.run_base[p.n_local];
             p.runs[1] = 0;
             p.runs[2 + sh.ex.run_base[p.n_local]] = n_active;
             p.meta[0] = total_chunks(p, sh.ex);
             p.meta[1] = n_active;
+            p.meta[2] = total_units(p, sh.ex);
         }
     }
     // rotations: items (o, chunk, proj) over the grouped order, grid-stride by wave
@@ -440,10 +478,12 @@ __global__ __launch_bounds__(1024) void moe_prepare_large_kernel(MoeParams p)
     if (!(p.mode & PREP_MOE)) return;
     if (p.has_shared)
         for (int r = t; r < p.T; r += 1024) p.order[n_active + r] = slots + r;
-    write_chunks(p, ex, p.chunks);
+    __syncthreads();                 // the shared rows of the order are read by write_chunks
+    write_chunks(p, ex, p.order);
     if (t == 0) {
         p.meta[0] = total_chunks(p, ex);
         p.meta[1] = n_active;
+        p.meta[2] = total_units(p, ex);
     }
 }
 
@@ -475,36 +515,37 @@ __device__ __forceinline__ const void* expert_ptr(const MoeParams& p, int e, int
 template <int TMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_kernel(MoeParams p, const half_t* __restrict__ xr)
 {
-    const int wid0 = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int nchunks = __builtin_amdgcn_readfirstlane(p.meta[0]);
+    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
     const int ncg = p.I / 128;
-    const int S = ks_gate_up(p, nchunks);
-    const int nslot = moe_nslot(p);
+    const KSplit k = ks_gate_up(p, units);
+    const int per_unit = 2 * ncg * k.base;
+    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * 2 * ncg)
+    const int u = wid / per_unit;
+    if (u >= units) return;
+    const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
+    const int* ch = p.chunks + 8 * ci;
+    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
+    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
+    const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
+    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
+    const int ubase = __builtin_amdgcn_readfirstlane(ch[4]);
+    const int S = ks_of_chunk(k, __builtin_amdgcn_readfirstlane(ch[5]));
+    const int r = wid - ubase * per_unit;
+    if (r >= 2 * ncg * S) return;
+    const int cg = r / (2 * S);
+    const int rem = r % (2 * S);
+    const int proj = rem / S, ks = rem % S;
+    const int* slot_of = p.order + begin;
+
     const int nch = p.H / 128;
-    // one item per wave: the launch covers max(gemv_waves, max_chunks * 2 * ncg) >= items
-    const int wid = wid0;
-    if (wid >= nchunks * 2 * ncg * S) return;
-    {
-        const int c = wid / (2 * ncg * S);
-        int rem = wid % (2 * ncg * S);
-        const int cg = rem / (2 * S);
-        rem %= 2 * S;
-        const int proj = rem / S, ks = rem % S;
-
-        const int* ch = p.chunks + 4 * c;
-        const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-        const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-        const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
-        const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
-        const int* slot_of = p.order + begin;
-
-        const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
-        const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, proj == 0 ? EVAMX_TBL_G_TRELLIS : EVAMX_TBL_U_TRELLIS);
-        const GlobalRows src{xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H,
-                             p.xsum + (size_t)proj * p.nslot_max * nch, nch};
-        float* part = p.part_gu + ((size_t)ks * 2 + proj) * nslot * p.I;
-        gemv_dispatch_k<TMAX>(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
-    }
+    const int nslot = moe_nslot(p);
+    const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
+    const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, proj == 0 ? EVAMX_TBL_G_TRELLIS : EVAMX_TBL_U_TRELLIS);
+    const GlobalRows src{xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch,
+                         nch};
+    float* part = p.part_gu + ((size_t)ks * 2 + proj) * nslot * p.I;
+    gemv_dispatch_k<TMAX>(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
 }
 
 // Activation epilogue: one wave per (grouped row o, 128-chunk a of I). Sums the gate/up
@@ -528,7 +569,8 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const half_t* u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
     const half_t* d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
     const float L = p.limit;
-    const int Sg = ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[0]));
+    const int Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
+                               __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
     const int nslot = moe_nslot(p);
     float g[2], u[2];
 #pragma unroll
@@ -598,33 +640,34 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
 template <int TMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_down_kernel(MoeParams p, const half_t* __restrict__ act)
 {
-    const int wid0 = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int nchunks = __builtin_amdgcn_readfirstlane(p.meta[0]);
+    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
     const int ncg = p.H / 128;
-    const int S = ks_down(p, nchunks);
-    const int nslot = moe_nslot(p);
+    const KSplit k = ks_down(p, units);
+    const int per_unit = ncg * k.base;
+    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * ncg)
+    const int u = wid / per_unit;
+    if (u >= units) return;
+    const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
+    const int* ch = p.chunks + 8 * ci;
+    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
+    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
+    const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
+    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
+    const int ubase = __builtin_amdgcn_readfirstlane(ch[4]);
+    const int S = ks_of_chunk(k, __builtin_amdgcn_readfirstlane(ch[5]));
+    const int r = wid - ubase * per_unit;
+    if (r >= ncg * S) return;
+    const int cg = r / S, ks = r % S;
+    const int* slot_of = p.order + begin;
+
     const int na = p.I / 128;
-    // one item per wave: the launch covers max(gemv_waves, max_chunks * ncg) >= items
-    const int wid = wid0;
-    if (wid >= nchunks * ncg * S) return;
-    {
-        const int c = wid / (ncg * S);
-        const int rem = wid % (ncg * S);
-        const int cg = rem / S, ks = rem % S;
-
-        const int* ch = p.chunks + 4 * c;
-        const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-        const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-        const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
-        const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
-        const int* slot_of = p.order + begin;
-
-        const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
-        const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, EVAMX_TBL_D_TRELLIS);
-        float* part = p.part_d + (size_t)ks * nslot * p.H;
-        gemv_dispatch_k<TMAX>(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{act, (size_t)p.I, p.actsum, na}, slot_of,
-                              tm, part, (size_t)p.H);
-    }
+    const int nslot = moe_nslot(p);
+    const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
+    const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, EVAMX_TBL_D_TRELLIS);
+    float* part = p.part_d + (size_t)ks * nslot * p.H;
+    gemv_dispatch_k<TMAX>(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{act, (size_t)p.I, p.actsum, na}, slot_of, tm,
+                          part, (size_t)p.H);
 }
 
 // Sum of the down k-split partials of slot s on this lane's two columns, fixed order; loads of
@@ -661,7 +704,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
     const int ncg = p.H / 128;
     const int row = blockIdx.x / ncg, cg = blockIdx.x % ncg;
     const int slots = p.T * p.topk;
-    const int S = ks_down(p, __builtin_amdgcn_readfirstlane(p.meta[0]));
+    const KSplit kd = ks_down(p, __builtin_amdgcn_readfirstlane(p.meta[2]));
     const int c0 = lane_col(lane, 0), c1 = lane_col(lane, 1);
     const int col0 = cg * 128 + c0, col1 = cg * 128 + c1;
     const int nitems = p.topk + (p.has_shared ? 1 : 0);
@@ -678,7 +721,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
         const float w = shared ? 1.0f : h2f(p.rw16[sk]);
         const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
         float v[2];
-        sum_partials(p, sk, cg, lane, S, v);
+        sum_partials(p, sk, cg, lane, ks_of_chunk(kd, p.slot_mult[sk]), v);
         if (shared) {
             v[0] = h2f(f2h(v[0]));                     // EXL3 linear C in fp16
             v[1] = h2f(f2h(v[1]));
@@ -743,7 +786,7 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
     const int tmax = tmax_for(p.T < EVAMX_CHUNK ? p.T : EVAMX_CHUNK);
     {
-        const int units = p.max_chunks * 2 * (p.I / 128);
+        const int units = EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128);
         const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
         const half_t* xr = p.xr;
         switch (tmax) {
@@ -758,7 +801,7 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         const int waves = nslot * (p.I / 128);
         hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
         mark(3);
-        const int units = p.max_chunks * (p.H / 128);
+        const int units = EVAMX_MAX_MULT * p.max_chunks * (p.H / 128);
         const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
         const half_t* act = p.act;
         switch (tmax) {
