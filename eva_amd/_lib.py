@@ -18,7 +18,7 @@ ABI_VERSION = 1
 EVAMX_OK, EVAMX_EINVAL, EVAMX_ELAUNCH, EVAMX_ENOSPACE = 0, -1, -2, -3
 DTYPE_F16, DTYPE_BF16 = 0, 1
 SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS = 0, 1
-ERR_EXPERT_RANGE = 1
+ERR_EXPERT_RANGE, ERR_RATE = 1, 2
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -11,7 +11,7 @@ Mirrors the reference's Python interface so callers switch by import:
   thread, the construction stream, a non-blocking lock, and any failure poisons the runner.
 
 Generalised as the DeepSeek-V3 shapes need: any hidden/inter (multiples of 128), top-k up to
-32, up to 512 local experts, rates 2/3/4/5 bits. ``packed`` is the ``[9, n_local]`` int64
+32, up to 512 local experts, rates 1.5 to 4 bits in steps of 0.5 and 5 bits. ``packed`` is the ``[9, n_local]`` int64
 pointer table (rows g_trellis, g_suh, g_svh, u_trellis, u_suh, u_svh, d_trellis, d_suh,
 d_svh; runtime/ds41/cache.py:1877-1886) or a sequence of its 9 rows.
 
@@ -33,7 +33,7 @@ import torch
 
 from . import ops
 
-RATES = (2, 3, 4, 5)
+RATES = (1.5, 2, 2.5, 3, 3.5, 4, 5)
 
 
 def _pointer_table(packed, device, n_local=None):

@@ -35,7 +35,7 @@ static int rate_k2(float bits)
     return -1;
 }
 
-static bool gemv_rate(int k2) { return k2 == 4 || k2 == 6 || k2 == 8 || k2 == 10; }
+static bool gemv_rate(int k2) { return gemv_k2_supported(k2); }   // 1.5 .. 4, 5 bits
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -181,7 +181,7 @@ extern "C" int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, 
     EVAMX_REQUIRE(rows >= 1 && rows <= 16, "evamx_exl3_linear: rows %d outside 1..16", rows);
     EVAMX_REQUIRE(in_features >= 128 && out_features >= 128 && in_features % 128 == 0 && out_features % 128 == 0,
                   "evamx_exl3_linear: in/out (%d, %d) must be positive multiples of 128", in_features, out_features);
-    EVAMX_REQUIRE(gemv_rate(k2), "evamx_exl3_linear: bit rate %g not in {2,3,4,5}", (double)bits);
+    EVAMX_REQUIRE(gemv_rate(k2), "evamx_exl3_linear: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)bits);
     const size_t need = linear_workspace(rows, in_features, out_features, nullptr, nullptr);
     if (workspace_bytes < need) {
         set_error("evamx_exl3_linear: workspace %zu bytes < %zu", workspace_bytes, need);
@@ -309,14 +309,14 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     int k2u = 0;
     if (!a->k2_per_expert) {
         k2u = rate_k2(a->bits);
-        EVAMX_REQUIRE(gemv_rate(k2u), "evamx_moe_forward: bit rate %g not in {2,3,4,5}", (double)a->bits);
+        EVAMX_REQUIRE(gemv_rate(k2u), "evamx_moe_forward: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)a->bits);
     }
     int k2s = 0;
     if (s->has_shared) {
         EVAMX_REQUIRE(a->shared, "evamx_moe_forward: shape has a shared expert but no pointers were given");
         for (int i = 0; i < 9; ++i) EVAMX_REQUIRE(a->shared[i] != 0, "evamx_moe_forward: shared pointer %d is null", i);
         k2s = rate_k2(a->shared_bits);
-        EVAMX_REQUIRE(gemv_rate(k2s), "evamx_moe_forward: shared bit rate %g not in {2,3,4,5}", (double)a->shared_bits);
+        EVAMX_REQUIRE(gemv_rate(k2s), "evamx_moe_forward: shared bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)a->shared_bits);
     }
     if (a->workspace_bytes < L.total) {
         set_error("evamx_moe_forward: workspace %zu bytes < %zu", a->workspace_bytes, L.total);

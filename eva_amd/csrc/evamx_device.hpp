@@ -14,6 +14,9 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int WAVE = 64;
+
+// Rates (k2 = 2 x bits) the decode GEMV is instantiated for: 1.5 .. 4 in steps of 0.5, and 5.
+__host__ __device__ constexpr bool gemv_k2_supported(int k2) { return (k2 >= 3 && k2 <= 8) || k2 == 10; }
 constexpr float R_SCALE = 0.088388347648f;   // 1/sqrt(128) as the reference spells it
 
 __device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, int s)
@@ -92,7 +95,7 @@ __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c)
 
 template <int K>
 struct LaneWords {
-    uint32_t b[K + 1];   // b[0] = previous word, b[1..K] = own words
+    uint32_t b[K + 1];   // b[0] = previous word of the tile's bit string, b[1..K] = own words
 };
 
 template <int K>
@@ -140,6 +143,36 @@ template <int K, int J>
 __device__ __forceinline__ half2_t lane_hpair(const LaneWords<K>& w)
 {
     return mul1_hpair(lane_hash<K, J>(w), lane_hash<K, J + 1>(w));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Half-integer rates b + 0.5 (exl3_dq.cuh:254-285): positions alternate b and b+1 bits, odd
+// positions carrying the extra bit. A lane's 32 positions then start 16*q*(2b+1) bits into the
+// tile, which is word-aligned for even q and half a word off for odd q. The lane normalises its
+// words into N[0..b] = the bit string from 16 bits before its first position (one v_alignbit
+// each, by 16 or 0 per lane), after which every window sits at a compile-time offset: position
+// j ends at bit 16 + (j odd ? (j+1)/2 * (2b+1) : j/2 * (2b+1) + b) of N.
+
+template <int B>
+constexpr int half_win_end(int j)
+{
+    return 16 + ((j & 1) ? ((j + 1) / 2) * (2 * B + 1) : (j / 2) * (2 * B + 1) + B);
+}
+
+template <int B, int J>
+__device__ __forceinline__ uint32_t half_hash(const uint32_t (&N)[B + 1])
+{
+    constexpr int E = half_win_end<B>(J);
+    constexpr int L = (E - 1) / 32;
+    constexpr int S = 32 * (L + 1) - E;
+    static_assert(L <= B, "window outside the normalised words");
+    return mul1_hash<false>(funnel(N[L > 0 ? L - 1 : 0], N[L], S));
+}
+
+template <int B, int J>
+__device__ __forceinline__ half2_t half_hpair(const uint32_t (&N)[B + 1])
+{
+    return mul1_hpair(half_hash<B, J>(N), half_hash<B, J + 1>(N));
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -53,22 +53,46 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const
     return (const __attribute__((address_space(1))) T*)p;
 }
 
-// A lane's K words with one non-temporal 64/96/128-bit global load (+1 dword at K=5).
+// A lane's words of one k-slice: its K words with one non-temporal 64/96/128-bit buffer load
+// (+1 dword at K=5), and the word before them in the tile's circular bit string (the last word
+// of the previous lane of the tile, or the tile's last word for the first lane) with one more
+// dword load from the same cache lines. Buffer loads take the wave-uniform slice offset in a
+// scalar register and the per-lane offsets as constant vector offsets, so a step spends no
+// vector instructions on addresses.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int BUF_NT = 2;                          // cache policy: non-temporal
+constexpr int BUF_WORD3 = 0x00020000;              // raw 32-bit buffer resource on gfx9-family parts
+
+// Resource of a wave-uniform base (the pointer is made provably uniform, so the descriptor lives
+// in scalar registers and no load needs a per-lane loop over descriptors).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const uint32_t* base)
+{
+    const uint64_t v = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    uint32_t* u = (uint32_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, 0x7fffffff, BUF_WORD3);
+}
+
 template <int K>
-__device__ __forceinline__ void load_words(LaneWords<K>& w, const uint32_t* p)
+__device__ __forceinline__ void load_slice(LaneWords<K>& w, __amdgpu_buffer_rsrc_t rsrc, uint32_t soff,
+                                           uint32_t lane_off, uint32_t prev_off)
 {
     if constexpr (K == 2) {
-        const u32x2a v = __builtin_nontemporal_load(gptr<u32x2a>(p));
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, lane_off, soff, BUF_NT));
         w.b[1] = v.x; w.b[2] = v.y;
     } else if constexpr (K == 3) {
-        const u32x3a v = __builtin_nontemporal_load(gptr<u32x3a>(p));
+        const u32x3 v = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rsrc, lane_off, soff, BUF_NT));
         w.b[1] = v.x; w.b[2] = v.y; w.b[3] = v.z;
     } else {
-        const u32x4a v = __builtin_nontemporal_load(gptr<u32x4a>(p));
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off, soff, BUF_NT));
         w.b[1] = v.x; w.b[2] = v.y; w.b[3] = v.z; w.b[4] = v.w;
 #pragma unroll
-        for (int i = 4; i < K; ++i) w.b[i + 1] = __builtin_nontemporal_load(gptr<uint32_t>(p + i));
+        for (int i = 4; i < K; ++i) w.b[i + 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, lane_off + 4 * i, soff, BUF_NT);
     }
+    w.b[0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, prev_off, soff, BUF_NT);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -87,31 +111,45 @@ struct GlobalRows {
 // Decode GEMV over one wave's k-range [16*kt0, 16*kt1): acc[m][h] = sum_k X[m][k] * h_k,
 // h_k = 1024 + bytesum of the weight at (k, col(lane, h)) (see mul1_hpair).
 
-// The previous word of a lane's tile run: lane (l & ~7) | ((l - 1) & 7)'s last word. DPP row
-// rotations within rows of 16 lanes: rotate by 1 serves lanes with l % 8 != 0, rotate by 9 the
-// first lane of each group of 8 (no LDS round trip, unlike a bpermute).
-__device__ __forceinline__ uint32_t prev_word(uint32_t v, int lane)
-{
-    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xf, 0xf, false);   // row_ror:1
-    const uint32_t r9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x129, 0xf, 0xf, false);   // row_ror:9
-    return (lane & 7) ? r1 : r9;
-}
-
 // Weight prefetch depth (k-slices in flight per wave): deeper for narrow chunks, whose loop
 // body is short; wide chunks keep register pressure in check.
 template <int TM>
 constexpr int prefetch_depth() { return TM <= 2 ? 7 : 4; }
 
-template <int K, int TM>
+// K2 = 2 x bits: even for integer rates (K = K2/2 words per lane), odd for rates b + 0.5.
+template <int K2, int TM>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
                                           const GlobalRows& src, const uint32_t (&aoff)[TM], int tm, float (&acc)[TM][2])
 {
-    constexpr int TW = 8 * K;
+    constexpr bool HALF = (K2 & 1) != 0;
+    constexpr int B = K2 / 2;                                // whole bits (half rates)
+    constexpr int K = HALF ? B + 1 : K2 / 2;                 // words loaded per lane besides b[0]
+    constexpr int TW = HALF ? 4 * (2 * B + 1) : 8 * K;       // words per tile
     constexpr int PF = prefetch_depth<TM>();
     const int lane = threadIdx.x & 63;
     const int q = lane & 7;
-    const size_t slice = (size_t)nt_n * TW;
-    const uint32_t* bp = trellis + (size_t)(cg * 8 + (lane >> 3)) * TW + q * K;
+    // the k-range is wave-uniform: keep it (and all index math below) in scalar registers
+    kt0 = __builtin_amdgcn_readfirstlane(kt0);
+    kt1 = __builtin_amdgcn_readfirstlane(kt1);
+    // byte offsets: slices are nt_n tiles apart, the wave's 8 tiles start at tile 8*cg; a
+    // projection is at most 7168 x 7168 x 8 bits, far below the 2 GiB buffer range
+    const uint32_t slice = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(nt_n * TW));
+    const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW));
+    const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(trellis);
+    uint32_t lane_off, prev_off;
+    uint32_t sh = 0;                                         // half rates: normalising shift
+    if constexpr (!HALF) {
+        lane_off = 4u * (uint32_t)((lane >> 3) * TW + q * K);
+        prev_off = 4u * (uint32_t)((lane >> 3) * TW + (q == 0 ? TW - 1 : q * K - 1));
+    } else {
+        // words s0 .. s0+B+1 cover the lane's bits and the 16 before them; s0 = -1 (q = 0) wraps
+        // to the tile's last word, which is loaded on its own like the integer rates' b[0]
+        const int r0 = 16 * q * (2 * B + 1);
+        const int s0 = (r0 - 17 + 32) / 32 - 1;              // floor((r0 - 17) / 32)
+        lane_off = 4u * (uint32_t)((lane >> 3) * TW + s0 + 1);
+        prev_off = 4u * (uint32_t)((lane >> 3) * TW + (q == 0 ? TW - 1 : s0));
+        sh = (q & 1) ? 0u : 16u;
+    }
 
 #pragma unroll
     for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = 0.0f;
@@ -121,7 +159,7 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
     LaneWords<K> ring[PF];
     const int last = kt1 - 1;
 #pragma unroll
-    for (int d = 0; d < PF; ++d) load_words<K>(ring[d], bp + (size_t)min(kt0 + d, last) * slice);
+    for (int d = 0; d < PF; ++d) load_slice<K>(ring[d], rsrc, cbase + (uint32_t)min(kt0 + d, last) * slice, lane_off, prev_off);
 
     // Narrow chunks load the next slice's activations (wave-uniform, scalar loads) one step
     // ahead, so their latency hides behind a decode instead of stalling every step.
@@ -145,20 +183,34 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
     auto step = [&](int kt, LaneWords<K>& w) {
         half2_t xn[TM][8];
         if constexpr (XPF) load_x(xn, min(kt + 1, last));
-        w.b[0] = prev_word(w.b[K], lane);
         half2_t wp[16];
+        if constexpr (!HALF) {
 #define EVAMX_DEC_UNIT(U)                                \
-        wp[4 * U + 0] = lane_hpair<K, 8 * U + 0>(w);     \
-        wp[4 * U + 1] = lane_hpair<K, 8 * U + 2>(w);     \
-        wp[4 * U + 2] = lane_hpair<K, 8 * U + 4>(w);     \
-        wp[4 * U + 3] = lane_hpair<K, 8 * U + 6>(w);
-        EVAMX_DEC_UNIT(0)
-        EVAMX_DEC_UNIT(1)
-        EVAMX_DEC_UNIT(2)
-        EVAMX_DEC_UNIT(3)
+            wp[4 * U + 0] = lane_hpair<K, 8 * U + 0>(w); \
+            wp[4 * U + 1] = lane_hpair<K, 8 * U + 2>(w); \
+            wp[4 * U + 2] = lane_hpair<K, 8 * U + 4>(w); \
+            wp[4 * U + 3] = lane_hpair<K, 8 * U + 6>(w);
+            EVAMX_DEC_UNIT(0)
+            EVAMX_DEC_UNIT(1)
+            EVAMX_DEC_UNIT(2)
+            EVAMX_DEC_UNIT(3)
 #undef EVAMX_DEC_UNIT
-        const int pre = __builtin_amdgcn_readfirstlane(min(kt + PF, last));
-        load_words<K>(w, bp + (size_t)pre * slice);
+        } else {
+            uint32_t N[B + 1];
+#pragma unroll
+            for (int k = 0; k <= B; ++k) N[k] = __builtin_amdgcn_alignbit(w.b[k], w.b[k + 1], sh);
+#define EVAMX_DEC_UNIT(U)                                \
+            wp[4 * U + 0] = half_hpair<B, 8 * U + 0>(N); \
+            wp[4 * U + 1] = half_hpair<B, 8 * U + 2>(N); \
+            wp[4 * U + 2] = half_hpair<B, 8 * U + 4>(N); \
+            wp[4 * U + 3] = half_hpair<B, 8 * U + 6>(N);
+            EVAMX_DEC_UNIT(0)
+            EVAMX_DEC_UNIT(1)
+            EVAMX_DEC_UNIT(2)
+            EVAMX_DEC_UNIT(3)
+#undef EVAMX_DEC_UNIT
+        }
+        load_slice<K>(w, rsrc, cbase + (uint32_t)min(kt + PF, last) * slice, lane_off, prev_off);
 #pragma unroll
         for (int m = 0; m < TM; ++m) {
             if (m < tm) {
@@ -208,7 +260,7 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
 // Only the row variants up to TMAX are compiled in, so a launch for narrow chunks is not
 // register-allocated for the widest one. A chunk of more than TMAX rows (possible only when
 // given routes repeat an expert within a token) is processed TMAX rows at a time.
-template <int K, int TMAX>
+template <int K2, int TMAX>
 __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
                                            const GlobalRows& src, const int* slot_of, int tm, float* part,
                                            size_t part_stride)
@@ -222,7 +274,7 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
             aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tr ? so[m] : so[0]) *        \
                                                                (int)(src.stride / 8));          \
         float acc[TMV][2];                                                                      \
-        gemv_wave<K, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, src, aoff, tr, acc);               \
+        gemv_wave<K2, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, src, aoff, tr, acc);               \
         _Pragma("unroll") for (int m = 0; m < TMV; ++m) {                                       \
             if (m < tr) {                                                                       \
                 const int row = so[m];                                                          \
@@ -256,18 +308,29 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
 #undef EVAMX_RUN
 }
 
-// Runtime rate (k2 = 2K) -> instantiated GEMV; integer rates 2..5.
+// Runtime rate (k2 = 2 x bits) -> instantiated GEMV: 1.5, 2, 2.5, 3, 3.5, 4, 5 bits. An
+// unsupported rate writes zero partials (the caller flags it), so no output reads stale data.
 template <int TMAX>
 __device__ __forceinline__ void gemv_dispatch_k(int k2, const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
                                                 const GlobalRows& src, const int* slot_of, int tm, float* part,
                                                 size_t part_stride)
 {
     switch (k2) {
-        case 4: gemv_chunk<2, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 6: gemv_chunk<3, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 8: gemv_chunk<4, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 10: gemv_chunk<5, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        default: break;
+        case 3: gemv_chunk<3, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 4: gemv_chunk<4, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 5: gemv_chunk<5, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 6: gemv_chunk<6, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 7: gemv_chunk<7, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 8: gemv_chunk<8, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        case 10: gemv_chunk<10, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
+        default: {
+            const int lane = threadIdx.x & 63;
+            for (int m = 0; m < tm; ++m) {
+                float* dst = part + (size_t)slot_of[m] * part_stride + cg * 128;
+                dst[lane_col(lane, 0)] = 0.0f;
+                dst[lane_col(lane, 1)] = 0.0f;
+            }
+        }
     }
 }
 

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int ncg = p.out / 128;
     if (wid >= ncg * p.ks) return;
-    const int cg = wid / p.ks, ks = wid % p.ks;
+    const int cg = __builtin_amdgcn_readfirstlane(wid / p.ks), ks = __builtin_amdgcn_readfirstlane(wid % p.ks);
     const int nch = p.in / 128;
     const int c0 = nch * ks / p.ks, c1 = nch * (ks + 1) / p.ks;
     gemv_dispatch_k<TMAX>(p.k2, p.trellis, p.out / 16, cg, c0, c1, GlobalRows{xr, (size_t)p.in, p.xsum, nch}, k_iota,

@@ -310,6 +310,7 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             c[1] = ex.off[e] + j * EVAMX_CHUNK;
             c[2] = rows;
             c[3] = p.k2_per_expert ? (int)p.k2_per_expert[e] : p.k2_uniform;
+            if (!gemv_k2_supported(c[3]) && j == 0) atomicOr(p.err, EVAMX_ERR_RATE);
             c[4] = u;
             c[5] = m;
             c[6] = 0;
@@ -521,7 +522,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     const KSplit k = ks_gate_up(p, units);
     const int per_unit = 2 * ncg * k.base;
     // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * 2 * ncg)
-    const int u = wid / per_unit;
+    const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
     if (u >= units) return;
     const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
     const int* ch = p.chunks + 8 * ci;
@@ -533,9 +534,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     const int S = ks_of_chunk(k, __builtin_amdgcn_readfirstlane(ch[5]));
     const int r = wid - ubase * per_unit;
     if (r >= 2 * ncg * S) return;
-    const int cg = r / (2 * S);
+    // integer division runs on the vector ALU: pin the (uniform) results to scalar registers
+    const int cg = __builtin_amdgcn_readfirstlane(r / (2 * S));
     const int rem = r % (2 * S);
-    const int proj = rem / S, ks = rem % S;
+    const int proj = __builtin_amdgcn_readfirstlane(rem / S), ks = __builtin_amdgcn_readfirstlane(rem % S);
     const int* slot_of = p.order + begin;
 
     const int nch = p.H / 128;
@@ -646,7 +648,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     const KSplit k = ks_down(p, units);
     const int per_unit = ncg * k.base;
     // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * ncg)
-    const int u = wid / per_unit;
+    const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
     if (u >= units) return;
     const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
     const int* ch = p.chunks + 8 * ci;
@@ -658,7 +660,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     const int S = ks_of_chunk(k, __builtin_amdgcn_readfirstlane(ch[5]));
     const int r = wid - ubase * per_unit;
     if (r >= ncg * S) return;
-    const int cg = r / S, ks = r % S;
+    const int cg = __builtin_amdgcn_readfirstlane(r / S), ks = __builtin_amdgcn_readfirstlane(r % S);
     const int* slot_of = p.order + begin;
 
     const int na = p.I / 128;

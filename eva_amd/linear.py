@@ -25,8 +25,8 @@ class ELinear:
         self.k = trellis.shape[-1] / 16
         if trellis.shape[0] * 16 != self.in_features or trellis.shape[1] * 16 != self.out_features:
             raise ValueError("trellis tiles disagree with suh/svh lengths")
-        if self.k not in (2, 3, 4, 5):
-            raise ValueError(f"EXL3 linear supports 2..5 bits, got {self.k}")
+        if self.k not in (1.5, 2, 2.5, 3, 3.5, 4, 5):
+            raise ValueError(f"EXL3 linear supports 1.5..4 bits in steps of 0.5 and 5 bits, got {self.k}")
         self._ws = None
 
     def _workspace(self, rows):

@@ -39,7 +39,7 @@ enum { EVAMX_OK = 0, EVAMX_EINVAL = -1, EVAMX_ELAUNCH = -2, EVAMX_ENOSPACE = -3 
 enum { EVAMX_DTYPE_F16 = 0, EVAMX_DTYPE_BF16 = 1 };
 enum { EVAMX_SCORE_SIGMOID = 0, EVAMX_SCORE_SQRT_SOFTPLUS = 1 };
 /* Device-side error flags (sticky bits in the workspace, read with evamx_moe_flags_ptr). */
-enum { EVAMX_ERR_EXPERT_RANGE = 1 };
+enum { EVAMX_ERR_EXPERT_RANGE = 1, EVAMX_ERR_RATE = 2 };
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* evamx_last_error(void);
@@ -59,7 +59,7 @@ int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, f
 size_t evamx_exl3_linear_workspace_bytes(int rows, int in_features, int out_features);
 
 /* y[rows][out] = svh * H(W^T H(x * suh)) with the reference's fp16 rounding points.
- * rows in 1..16; in/out multiples of 128; bits in {2,3,4,5}. All pointers device. */
+ * rows in 1..16; in/out multiples of 128; bits in {1.5,2,2.5,3,3.5,4,5}. All pointers device. */
 int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, int out_features,
                       const void* trellis, const void* suh_fp16, const void* svh_fp16, float bits,
                       void* y_fp16, void* workspace, size_t workspace_bytes, evamx_stream_t stream);
@@ -123,8 +123,10 @@ typedef struct evamx_moe_args {
     /* experts */
     const int64_t* tables;        /* device int64 [9][n_local]: g_trellis, g_suh, g_svh,
                                      u_trellis, u_suh, u_svh, d_trellis, d_suh, d_svh */
-    const uint8_t* k2_per_expert; /* device [n_local], 2*bits per expert, or NULL */
-    float bits;                   /* uniform rate when k2_per_expert is NULL: 2, 3, 4, 5 */
+    const uint8_t* k2_per_expert; /* device [n_local], 2*bits per expert (3..8 or 10), or NULL;
+                                     another value sets EVAMX_ERR_RATE and the expert adds 0 */
+    float bits;                   /* uniform rate when k2_per_expert is NULL: 1.5 .. 4 in steps
+                                     of 0.5, or 5 */
     const int64_t* shared;        /* HOST array of 9 device pointers (table order) or NULL */
     float shared_bits;
     float limit;                  /* SwiGLU limit (0: none) */

@@ -77,4 +77,5 @@ def logits_zipf(rng, t, n_experts, s=1.1):
 
 
 def mixed_rates(rng, n_experts, rates=(2, 3, 4, 5)):
+    """Per-expert rates drawn uniformly from ``rates`` (config 4: {2,3,4,5})."""
     return rng.choice(np.array(rates, dtype=np.float64), size=n_experts)

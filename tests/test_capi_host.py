@@ -92,7 +92,7 @@ def _args(**kw):
 @pytest.mark.parametrize("bad,msg", [
     (dict(rows=0), "rows"), (dict(rows=5), "rows"), (dict(x=0), "null"), (dict(out=0), "null"),
     (dict(x_dtype=7), "x_dtype"), (dict(x_stride=100), "strides"), (dict(limit=-1.0), "limit"),
-    (dict(limit=float("inf")), "limit"), (dict(bits=2.5), "bit rate"), (dict(bits=6.0), "bit rate"),
+    (dict(limit=float("inf")), "limit"), (dict(bits=1.0), "bit rate"), (dict(bits=6.0), "bit rate"), (dict(bits=4.5), "bit rate"),
     (dict(weights=0), "weights"), (dict(min_expert=4, max_expert=4), "range"),
     (dict(logits=FAKE, n_logits=4), "n_logits"), (dict(logits=FAKE, n_logits=256, score_fn=3), "score"),
 ])

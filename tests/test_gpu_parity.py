@@ -72,7 +72,7 @@ def test_prepare_routes_bit_exact(dev, rows, topk, n_local, zero_frac):
     assert np.array_equal(runs, ref)
 
 
-@pytest.mark.parametrize("K", [2, 3, 4, 5])
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
 @pytest.mark.parametrize("rows", [1, 3, 16])
 def test_exl3_linear(dev, K, rows):
     ops = _ops()
@@ -94,11 +94,11 @@ def _layer_case(rng, H, I, E, K, svh_scale, rates=None):
 
 
 @pytest.mark.parametrize("rows", [1, 2, 5, 16])
-@pytest.mark.parametrize("K", [2, 3, 4, 5])
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
 def test_moe_layer_small(dev, rows, K):
     ops = _ops()
     H, I, E, topk, limit = 512, 256, 24, 4, 10.0
-    rng = np.random.default_rng(1000 * rows + K)
+    rng = np.random.default_rng(int(1000 * rows + 2 * K))
     experts, shared = _layer_case(rng, H, I, E, K, 1 / np.sqrt(H))
     x = synth.activations_bf16(rng, rows, H)
     logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
@@ -158,11 +158,12 @@ def test_moe_layer_dsv3_shape(dev, rows):
     assert rel_err_rows(out.cpu().numpy(), ref) < TOL
 
 
-def test_moe_mixed_rates_and_given_routes(dev):
+@pytest.mark.parametrize("rate_set", [(2, 3, 4, 5), (1.5, 2.5, 3.5, 4)])
+def test_moe_mixed_rates_and_given_routes(dev, rate_set):
     ops = _ops()
     H, I, E, topk, limit = 256, 256, 10, 3, 0.0
-    rng = np.random.default_rng(5)
-    rates = synth.mixed_rates(rng, E)
+    rng = np.random.default_rng(5 + len(rate_set) + int(2 * rate_set[0]))
+    rates = synth.mixed_rates(rng, E, rate_set)
     experts, _ = _layer_case(rng, H, I, E, 4, 1 / np.sqrt(H), rates)
     rows = 7
     x = rng.standard_normal((rows, H)).astype(np.float16)
