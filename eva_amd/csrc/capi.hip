@@ -150,7 +150,7 @@ using namespace evamx;
 
 extern "C" const char* evamx_last_error(void) { return g_err; }
 
-extern "C" int evamx_abi_version(void) { return 1; }
+extern "C" int evamx_abi_version(void) { return 2; }
 
 extern "C" int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, float bits, void* w_fp16,
                                   evamx_stream_t stream)
@@ -290,9 +290,12 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     if (!shape_ok(s)) return EVAMX_EINVAL;
     const MoeLayout L = moe_layout(s);
     EVAMX_REQUIRE(a->rows >= 1 && a->rows <= s->rows_max, "evamx_moe_forward: rows %d outside 1..%d", a->rows, s->rows_max);
-    EVAMX_REQUIRE(a->x && a->out && a->tables && a->sel && a->workspace, "evamx_moe_forward: null pointer");
+    EVAMX_REQUIRE(a->x && (a->out || a->residual) && a->tables && a->sel && a->workspace,
+                  "evamx_moe_forward: null pointer");
     EVAMX_REQUIRE(a->x_dtype == EVAMX_DTYPE_F16 || a->x_dtype == EVAMX_DTYPE_BF16, "evamx_moe_forward: x_dtype %d", a->x_dtype);
-    EVAMX_REQUIRE(a->x_stride >= s->hidden && a->out_stride >= s->hidden, "evamx_moe_forward: row strides below hidden");
+    EVAMX_REQUIRE(a->x_stride >= s->hidden && (!a->out || a->out_stride >= s->hidden) &&
+                      (!a->residual || a->residual_stride >= s->hidden),
+                  "evamx_moe_forward: row strides below hidden");
     EVAMX_REQUIRE(std::isfinite(a->limit) && a->limit >= 0.0f, "evamx_moe_forward: limit must be finite and >= 0");
     if (a->logits) {
         EVAMX_REQUIRE(a->n_logits >= s->topk && a->n_logits <= EVAMX_MAX_EXPERTS,
@@ -365,6 +368,7 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.cap_rows_gu = L.cap_rows_gu; p.cap_rows_d = L.cap_rows_d;
     p.gemv_waves = gemv_waves();
     p.out = a->out; p.out_stride = a->out_stride;
+    p.residual = (uint16_t*)a->residual; p.residual_stride = a->residual_stride;
     moe_launch(p, (hipStream_t)stream, a->events);
     return launched("moe_forward");
 }

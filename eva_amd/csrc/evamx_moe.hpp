@@ -67,8 +67,10 @@ struct MoeParams {
     int cap_rows_gu, cap_rows_d;   // partial-buffer capacity in rows (ks * nslot <= cap)
     int gemv_waves;            // grid of the GEMV kernels (waves resident on the device at once)
     // output
-    float* out;
+    float* out;                // or null
     int out_stride;
+    uint16_t* residual;        // bf16, updated in place, or null
+    int residual_stride;
 };
 
 // Rows of the GEMV partial buffers in this call: the routed slots, then the shared expert's rows.

@@ -81,6 +81,15 @@ __device__ float route_weight(float s, float tot, float scale)
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
 
+// bf16 <-> fp32 with round-to-nearest-even (finite values; NaN stays NaN)
+__device__ __forceinline__ float bf16_value(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t bf16_bits(float f)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 __device__ __forceinline__ half_t load_x16(const void* x, int dtype, size_t i)
 {
     if (dtype == EVAMX_DTYPE_F16) return ((const half_t*)x)[i];
@@ -750,9 +759,17 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
             o0 = o0 + part[p.topk][c0];
             o1 = o1 + part[p.topk][c1];
         }
-        float* dst = p.out + (size_t)row * p.out_stride;
-        dst[col0] = o0;
-        dst[col1] = o1;
+        if (p.out) {
+            float* dst = p.out + (size_t)row * p.out_stride;
+            dst[col0] = o0;
+            dst[col1] = o1;
+        }
+        if (p.residual) {
+            // h = bf16(h + bf16(y)): y cast to the activation dtype, then the bf16 add
+            uint16_t* h = p.residual + (size_t)row * p.residual_stride;
+            h[col0] = bf16_bits(bf16_value(h[col0]) + bf16_value(bf16_bits(o0)));
+            h[col1] = bf16_bits(bf16_value(h[col1]) + bf16_value(bf16_bits(o1)));
+        }
     }
 }
 

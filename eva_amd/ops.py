@@ -146,26 +146,35 @@ class MoeWorkspace:
         return self.buffer[off:off + 4].view(torch.int32)
 
 
-def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: torch.Tensor, *, limit: float,
+def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: torch.Tensor | None, *, limit: float,
                 bits: float | None = None, k2_per_expert: torch.Tensor | None = None,
                 logits: torch.Tensor | None = None, sel: torch.Tensor | None = None,
                 weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
                 score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
                 shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0,
-                events=None):
+                events=None, residual: torch.Tensor | None = None):
     """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
 
     With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
     must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
     the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
     ``events``: optional ctypes array of 6 hipEvent_t handles recorded around the 5 stages.
+    ``residual``: optional bf16 ``[rows, H]`` stream updated in place to ``bf16(residual + bf16(y))``
+    (may be ``x`` itself); ``out`` may then be None.
     """
     s = ws.shape
     _dev(x, "x", None, 2, row_strided=True)
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("x must be fp16 or bf16")
     _dev(tables, "tables", torch.int64, 2)
-    _dev(out, "out", torch.float32, 2, row_strided=True)
+    if out is None and residual is None:
+        raise ValueError("need out, residual or both")
+    if out is not None:
+        _dev(out, "out", torch.float32, 2, row_strided=True)
+    if residual is not None:
+        _dev(residual, "residual", torch.bfloat16, 2, row_strided=True)
+        if residual.shape[0] != x.shape[0] or residual.shape[1] < s.hidden:
+            raise ValueError("residual must be [rows, >= hidden]")
     if tables.shape != (9, s.n_local):
         raise ValueError(f"tables must be [9, {s.n_local}]")
     rows = x.shape[0]
@@ -197,7 +206,10 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
         a.shared_bits = float(shared_bits)
     a.limit = float(limit)
     a.out = ptr(out)
-    a.out_stride = out.stride(0)
+    a.out_stride = out.stride(0) if out is not None else 0
+    if residual is not None:
+        a.residual = ptr(residual)
+        a.residual_stride = residual.stride(0)
     a.workspace = ptr(ws.buffer)
     a.workspace_bytes = ws.buffer.numel()
     if events is not None:

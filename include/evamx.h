@@ -131,7 +131,7 @@ typedef struct evamx_moe_args {
     float shared_bits;
     float limit;                  /* SwiGLU limit (0: none) */
     /* output: out[r][0..hidden) = routed (slot order, fp32) + shared */
-    float* out;                   /* device */
+    float* out;                   /* device, or NULL when residual is given */
     int32_t out_stride;           /* elements; >= hidden */
     void* workspace;              /* device, evamx_moe_workspace_bytes(&shape) bytes */
     size_t workspace_bytes;
@@ -139,6 +139,11 @@ typedef struct evamx_moe_args {
      * gate/up GEMV, activation, down GEMV, combine): events[i] before stage i, events[5]
      * after the last; NULL for none */
     void* const* events;
+    /* optional residual stream: bf16 [rows][residual_stride], updated in place to
+     * bf16(residual + bf16(out)) (the layer output cast to the activation dtype and added,
+     * model.py:499); may be the x of this call. NULL for none. */
+    void* residual;
+    int32_t residual_stride;      /* elements; >= hidden */
 } evamx_moe_args;
 
 size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape);

@@ -361,6 +361,32 @@ def moe_layer(x, logits, experts, shared, topk, limit, score_fn="sigmoid", sel_b
     return y, idx, w, rw
 
 
+def round_bf16(v):
+    """fp32 -> nearest bf16 (ties to even), returned as float32 values."""
+    x = np.ascontiguousarray(np.asarray(v, dtype=np.float32))
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def residual_add(h_bf16, y):
+    """model.py:499 then the residual: ``h + y.to(bf16)`` in bf16 (fp32 add, one rounding)."""
+    return round_bf16(np.asarray(h_bf16, np.float32) + round_bf16(y))
+
+
+def layer_stack(h_bf16, logits, layers, topk, limit, score_fn="sigmoid"):
+    """Config 5: MoE layers applied in turn with a bf16 residual stream.
+
+    ``logits[l]`` routes layer l (independent of h, as the configuration draws them);
+    ``layers[l] = (experts, shared)``. Returns the final bf16 stream (as float32 values).
+    """
+    h = round_bf16(h_bf16)
+    for l, (experts, shared) in enumerate(layers):
+        y, _, _, _ = moe_layer(h, logits[l], experts, shared, topk, limit, score_fn)
+        h = residual_add(h, y)
+    return h
+
+
 def rel_err_rows(y, ref):
     """max_r ( max|y_r - ref_r| / max|ref_r| ): the tolerance metric for layer outputs."""
     y = np.asarray(y, dtype=np.float64)
