@@ -10,6 +10,12 @@ Cache hygiene: the weights of L layer copies (257 experts each, 5.7 GB per layer
 resident and every step uses the next layer and a fresh routing draw, so a step's 199 MB are
 not served from the 256 MiB MALL. Steps are replayed from a hipGraph.
 
+Other configurations (extra lines, same JSON keys):
+  --tokens 16                 configs[2]: 16 tokens, per-token-bias routing
+  --workload prefill          configs[3]: 512 tokens, Zipf(1.1) routing, per-expert rates {2,3,4,5}
+  --workload stack            configs[4]: 58 stacked layers at 2.5 bpw (all 257 x 58 experts
+                              resident, ~205 GB), 8 tokens, bf16 residual, one hipGraph per step
+
 Output: one JSON line (value = achieved HBM GB/s over the algorithmic bytes of the step).
 """
 from __future__ import annotations
@@ -29,6 +35,12 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE layer decode µs + achieved HBM GB/s (DSv3 shape, 4bpw EXL3, 1/16 tok)"
 PEAK_HBM = 8000.0         # GB/s, MI355X
 H, I, E, TOPK = 7168, 2048, 256, 8
+STACK_DOWN_SCALE = 0.25   # down-projection svh multiplier of the stacked workload (see DeviceLayers)
+
+
+def tile_u16(bits):
+    b = float(bits)
+    return 16 * int(b) + 8 if b != int(b) else 16 * int(b)
 
 
 def proj_bytes(n_in, n_out, bits):
@@ -44,37 +56,61 @@ def log(msg):
 
 
 class DeviceLayers:
-    """L layers x (E routed + 1 shared) experts, all resident, with [9, E] pointer tables."""
+    """L layers x (E routed + 1 shared) experts, all resident, with [9, E] pointer tables.
 
-    def __init__(self, torch, dev, n_layers, bits, hidden=H, inter=I, n_experts=E, seed=1234):
+    ``rates``: one rate for every expert, or a callable (layer, expert) -> rate for mixed
+    rates (then ``k2[l]`` is the layer's uint8 [E] table of 2 x bits; the shared expert keeps
+    ``shared_bits``). ``down_scale`` multiplies the down projections' svh (a stack of layers
+    without norms keeps its residual stream O(1) only if each layer's output is small: SwiGLU
+    makes the output quadratic in the input, and fp16 gate/up outputs overflow otherwise)."""
+
+    def __init__(self, torch, dev, n_layers, rates, hidden=H, inter=I, n_experts=E, seed=1234, shared_bits=None,
+                 down_scale=1.0):
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         self.n = n_experts + 1
-        t16 = int(16 * bits)
-        self.proj_elems = (hidden // 16) * (inter // 16) * t16
-        nbig = n_layers * self.n * 3 * self.proj_elems
-        log(f"allocating {nbig * 2 / 1e9:.1f} GB of trellis for {n_layers} layers")
-        self.trellis = torch.empty(nbig, dtype=torch.int16, device=dev)
+        if callable(rates):
+            rate_of = rates
+            self.mixed = True
+        else:
+            rate_of = (lambda l, e, r=float(rates): r)
+            self.mixed = False
+        sb = float(shared_bits) if shared_bits is not None else None
+        self.rates = [[float(rate_of(l, e)) if e < n_experts or sb is None else sb for e in range(self.n)]
+                      for l in range(n_layers)]
+        tiles_gu = (hidden // 16) * (inter // 16)        # tiles per projection (all three equal)
+        offs, total = [], 0
+        for l in range(n_layers):
+            row = []
+            for e in range(self.n):
+                row.append(total)
+                total += 3 * tiles_gu * tile_u16(self.rates[l][e])
+            offs.append(row)
+        log(f"allocating {total * 2 / 1e9:.1f} GB of trellis for {n_layers} layer(s)")
+        self.trellis = torch.empty(total, dtype=torch.int16, device=dev)
         chunk = 1 << 28
-        for s in range(0, nbig, chunk):
+        for s in range(0, total, chunk):
             self.trellis[s:s + chunk].random_(-32768, 32768, generator=g)
         vec = max(hidden, inter)
         self.suh = (torch.randint(0, 2, (n_layers, self.n, 3, vec), generator=g, device=dev) * 2 - 1).half()
         mag = torch.rand((n_layers, self.n, 3, vec), generator=g, device=dev) + 0.5
         sign = torch.randint(0, 2, (n_layers, self.n, 3, vec), generator=g, device=dev) * 2 - 1
+        mag[:, :, 2] *= down_scale
         self.svh = (mag * sign / (hidden ** 0.5)).half()
+        del mag, sign
         base_t = self.trellis.data_ptr()
         base_su = self.suh.data_ptr()
         base_sv = self.svh.data_ptr()
-        self.tables, self.shared = [], []
+        self.tables, self.shared, self.k2 = [], [], []
         for l in range(n_layers):
             rows = [[0] * n_experts for _ in range(9)]
             sh = [0] * 9
             for e in range(self.n):
+                pe = tiles_gu * tile_u16(self.rates[l][e])
                 ptrs = []
                 for p in range(3):
                     k = (l * self.n + e) * 3 + p
-                    ptrs += [base_t + 2 * k * self.proj_elems, base_su + 2 * k * vec, base_sv + 2 * k * vec]
+                    ptrs += [base_t + 2 * (offs[l][e] + p * pe), base_su + 2 * k * vec, base_sv + 2 * k * vec]
                 if e < n_experts:
                     for r in range(9):
                         rows[r][e] = ptrs[r]
@@ -82,11 +118,20 @@ class DeviceLayers:
                     sh = ptrs
             self.tables.append(torch.tensor(rows, dtype=torch.int64, device=dev))
             self.shared.append(sh)
+            self.k2.append(torch.tensor([int(round(2 * r)) for r in self.rates[l][:n_experts]],
+                                        dtype=torch.uint8, device=dev) if self.mixed else None)
+
+    def step_bytes(self, l, experts):
+        """Algorithmic weight bytes of layer l for the given routed experts plus the shared one."""
+        return sum(expert_bytes(self.rates[l][e]) for e in experts) + expert_bytes(self.rates[l][-1])
+
+    def gate_up_bytes(self, l, experts):
+        return sum(2 * proj_bytes(H, I, self.rates[l][e]) for e in list(experts) + [self.n - 1])
 
 
-def cpu_baseline(seconds_hint=True):
-    """PyTorch-CPU restatement on the host cores: one routed expert + the shared expert of the
-    1-token layer (the sampled bytes are 2 of the 9 experts the full step reads)."""
+def cpu_baseline(bits=4.0, tokens=1, n_routed=1, min_seconds=10.0):
+    """PyTorch-CPU restatement on the host cores: ``n_routed`` routed experts + the shared
+    expert of a ``tokens``-token layer at ``bits`` (a bounded sample of the GPU workload)."""
     import numpy as np
     import torch
 
@@ -95,45 +140,49 @@ def cpu_baseline(seconds_hint=True):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     rng = np.random.default_rng(5)
-    ew = [synth.expert(rng, H, I, 4, 1 / np.sqrt(H)) for _ in range(2)]
+    ew = [synth.expert(rng, H, I, bits, 1 / np.sqrt(H)) for _ in range(n_routed + 1)]
     parts = [tuple(tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in ew_i.parts[p]) for p in "gud") for ew_i in ew]
-    dec = torch_cpu.Decoder(4)
-    x = torch.from_numpy(synth.activations_bf16(rng, 1, H))
-    idx = torch.tensor([[0]])
-    w = torch.tensor([[1.0]])
+    dec = torch_cpu.Decoder(bits)
+    x = torch.from_numpy(synth.activations_bf16(rng, tokens, H))
+    idx = torch.tensor([[e for e in range(n_routed)]] * tokens)
+    w = torch.full((tokens, n_routed), 1.0 / n_routed)
+    experts = {e: parts[e] for e in range(n_routed)}
 
     def run():
-        return torch_cpu.moe_layer(x, idx, w, {0: parts[0]}, parts[1], dec, 10.0)
+        return torch_cpu.moe_layer(x, idx, w, experts, parts[n_routed], dec, 10.0)
 
     run()                                   # warm-up
     times = []
-    while len(times) < 2 or (sum(times) < 10.0 and len(times) < 12):
+    while len(times) < 2 or (sum(times) < min_seconds and len(times) < 12):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
     t = sum(times) / len(times)
-    nbytes = 2 * expert_bytes(4)
+    nbytes = (n_routed + 1) * expert_bytes(bits)
     model = ""
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:
         pass
     return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"1 routed + 1 shared expert of the 1-token DSv3 layer at 4 bpw "
+            "sample": f"{n_routed} routed + 1 shared expert of a {tokens}-token DSv3 layer at {bits:g} bpw "
                       f"({nbytes / 1e6:.1f} MB; mean of {len(times)} runs after 1 warm-up; {t:.2f} s each, "
                       f"{sum(times):.1f} s timed)",
-            "layer_seconds_scaled": round(t * 9 / 2, 2), "cpu_model": model,
-            "torch_threads": torch.get_num_threads()}
+            "seconds_per_sample": round(t, 3), "cpu_model": model, "torch_threads": torch.get_num_threads()}
 
 
-def main():
+def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--tokens", type=int, default=1)
-    ap.add_argument("--bits", type=float, default=4.0)
-    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--workload", choices=("layer", "stack", "prefill"), default="layer",
+                    help="layer: one decode layer (configs[1] at 1 token, configs[2] at 16); stack: configs[4], "
+                         "58 stacked layers at 2.5 bpw, 8 tokens, one hipGraph; prefill: configs[3], 512 tokens, "
+                         "Zipf routing, per-expert rates {2,3,4,5}")
+    ap.add_argument("--tokens", type=int, default=None)
+    ap.add_argument("--bits", type=float, default=None)
+    ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--graph-steps", type=int, default=8)
     ap.add_argument("--ksplit-gu", type=int, default=0)
     ap.add_argument("--ksplit-down", type=int, default=0)
@@ -144,6 +193,18 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    defaults = {"layer": (1, 4.0, 4), "stack": (8, 2.5, 58), "prefill": (512, None, 2)}[args.workload]
+    if args.tokens is None:
+        args.tokens = defaults[0]
+    if args.bits is None:
+        args.bits = defaults[1]
+    if args.layers is None:
+        args.layers = defaults[2]
+    return args
+
+
+def main():
+    args = parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, "
               "'How the path would shard'); run with --gpus 1", file=sys.stderr)
@@ -154,20 +215,16 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch)
         return
+    if args.workload == "stack":
+        result = run_stack(torch, args)
+    else:
+        result = run_layer(torch, args)
+    print(json.dumps(result), flush=True)
 
-    from eva_amd import ops
-    from eva_amd._lib import lib
 
-    dev = torch.device("cuda", 0)
-    T = args.tokens
-    if args.routing is None:
-        args.routing = "plain" if T == 1 else "skewed"
-    layers = DeviceLayers(torch, dev, args.layers, args.bits)
-    g = torch.Generator(device=dev)
-    g.manual_seed(99)
-    n_draws = max(args.graph_steps, args.layers) * 2
+def make_logits(torch, g, dev, n_draws, T, routing):
     logits = torch.randn((n_draws, T, E), generator=g, device=dev)
-    if args.routing == "skewed":
+    if routing == "skewed":
         # config 3: per-token random bias so expert loads span 0..T (2 hot experts +6 for every
         # token, 6 warm experts +3 for a per-token coin flip, a fresh draw of both per step)
         for i in range(n_draws):
@@ -175,30 +232,80 @@ def main():
             logits[i][:, perm[:2]] += 6.0
             coin = torch.randint(0, 2, (T, 6), generator=g, device=dev).float()
             logits[i][:, perm[2:8]] += 3.0 * coin
+    elif routing == "zipf":
+        # config 4: Zipf(1.1) over a random expert permutation, 8 distinct picks per token
+        # (log p + Gumbel noise: its top-k is a draw without replacement with probabilities p)
+        ranks = torch.arange(1, E + 1, dtype=torch.float64, device=dev)
+        logp = torch.log(ranks ** -1.1 / (ranks ** -1.1).sum())
+        for i in range(n_draws):
+            perm = torch.randperm(E, generator=g, device=dev)
+            lp = torch.empty(E, dtype=torch.float64, device=dev)
+            lp[perm] = logp
+            u = torch.rand((T, E), generator=g, device=dev, dtype=torch.float64).clamp_(1e-300, 1.0)
+            logits[i] = (lp[None, :] - torch.log(-torch.log(u))).float()
+    return logits
+
+
+def timed_replays(torch, stream, run_block, reps, warm):
+    run_block(warm)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    run_block(reps)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1)
+
+
+def run_layer(torch, args):
+    """One MoE layer per step, cycling resident layers."""
+    from eva_amd import ops
+    from eva_amd._lib import lib
+
+    dev = torch.device("cuda", 0)
+    T = args.tokens
+    prefill = args.workload == "prefill"
+    if args.routing is None:
+        args.routing = "zipf" if prefill else ("plain" if T == 1 else "skewed")
+    if prefill:
+        rng_rates = torch.Generator().manual_seed(4321)
+        rate_tab = [[float((2, 3, 4, 5)[int(v)]) for v in torch.randint(0, 4, (E,), generator=rng_rates)]
+                    for _ in range(args.layers)]
+        layers = DeviceLayers(torch, dev, args.layers, lambda l, e: rate_tab[l][e], shared_bits=4.0)
+    else:
+        layers = DeviceLayers(torch, dev, args.layers, args.bits)
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    G = 1 if prefill else args.graph_steps
+    n_draws = max(G, args.layers) * 2
+    logits = make_logits(torch, g, dev, n_draws, T, args.routing)
     x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
     ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
                           ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down)
     sel = torch.empty(T, TOPK, dtype=torch.int64, device=dev)
     wts = torch.empty(T, TOPK, dtype=torch.float32, device=dev)
     out = torch.empty(T, H, dtype=torch.float32, device=dev)
+    shared_bits = 4.0 if prefill else args.bits
 
-    def step(i):
+    def step(i, events=None):
         l = i % args.layers
-        ops.moe_forward(ws, x, layers.tables[l], out, limit=10.0, bits=args.bits, logits=logits[i % n_draws],
-                        sel=sel, weights=wts, shared_ptrs=layers.shared[l], shared_bits=args.bits)
+        ops.moe_forward(ws, x, layers.tables[l], out, limit=10.0, bits=None if prefill else args.bits,
+                        k2_per_expert=layers.k2[l], logits=logits[i % n_draws], sel=sel, weights=wts,
+                        shared_ptrs=layers.shared[l], shared_bits=shared_bits, events=events)
 
-    # unique experts per step (for the algorithmic bytes), from the same routing draws
-    uniq = []
+    # experts touched per step (for the algorithmic bytes), from the same routing draws
+    touched = []
     for i in range(n_draws):
         step(i)
-        uniq.append(len(set(sel.reshape(-1).tolist())))
+        touched.append(sorted(set(sel.reshape(-1).tolist())))
     torch.cuda.synchronize()
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite layer output")
-    ebytes = expert_bytes(args.bits)
+    if int(ws.flags().cpu()[0]) != 0:
+        raise RuntimeError(f"device error flags {int(ws.flags().cpu()[0])}")
     act_bytes = T * H * 2 + T * E * 4 + T * H * 4
 
-    G = args.graph_steps
     stream = torch.cuda.Stream(device=dev)
     graph = None
     if not args.no_graph:
@@ -212,8 +319,8 @@ def main():
                     step(i)
     reps = max(1, args.steps // G)
     steps = reps * G
-    mean_uniq = sum(uniq[i % n_draws] for i in range(G)) / G
-    step_bytes = (mean_uniq + 1) * ebytes + act_bytes
+    step_bytes = sum(layers.step_bytes(i % args.layers, touched[i % n_draws]) for i in range(G)) / G + act_bytes
+    mean_uniq = sum(len(touched[i % n_draws]) for i in range(G)) / G
 
     def run_block(n):
         with torch.cuda.stream(stream):
@@ -224,50 +331,133 @@ def main():
                 for i in range(n * G):
                     step(i)
 
-    run_block(max(1, args.warmup // G))
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    run_block(reps)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1)
+    ms = timed_replays(torch, stream, run_block, reps, max(1, args.warmup // G))
     us_step = ms * 1e3 / steps
     gbps = step_bytes / (us_step * 1e-6) / 1e9
     log(f"{steps} steps, {us_step:.2f} us/step, {gbps:.1f} GB/s (unique experts/step {mean_uniq:.1f})")
 
     # Per-kernel durations on the launch stream (eager pass, events between the launches).
-    kt = kernel_times(torch, ops, lib, ws, x, layers, logits, sel, wts, out, args, stream, n_draws)
-    gu_bytes_launch = (mean_uniq + 1) * 2 * proj_bytes(H, I, args.bits)
-    gu_us = kt["moe_gate_up"]
-    roofline = {"bound": "hbm", "kernel": "moe_gate_up",
-                "achieved": round(gu_bytes_launch / (gu_us * 1e-6) / 1e9, 1),
-                "peak": PEAK_HBM, "unit": "GB/s",
-                "frac": round(gu_bytes_launch / (gu_us * 1e-6) / 1e9 / PEAK_HBM, 4),
-                "traffic": measured_traffic(T, args.bits),
-                "algorithmic_bytes_per_launch": int(gu_bytes_launch),
-                "avg_launch_us": round(gu_us, 3)}
-
+    n_ev = 16 if prefill else 64
+    kt = kernel_times(torch, stream, step, n_ev, skip=2 if prefill else 8)
+    gu_bytes_launch = sum(layers.gate_up_bytes(i % args.layers, touched[i % n_draws]) for i in range(n_ev)) / n_ev
+    roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, args.bits))
+    cfg_idx = 3 if prefill else (1 if T == 1 else 2)
+    rates = "per-expert rates {2,3,4,5} (shared 4)" if prefill else f"{args.bits:g} bpw"
     result = {
         "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 6), "us_per_layer": round(us_step, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5)/sqrt(H) svh, N(0,1) logits, bf16 N(0,1) x)",
-        "config": {"workload": f"DSv3 MoE layer decode, {T} token(s), {args.bits:g} bpw EXL3 "
-                               f"(BASELINE configs[{1 if T == 1 else 2}])", "routing": args.routing,
+        "config": {"workload": f"DSv3 MoE layer {'prefill' if prefill else 'decode'}, {T} token(s), {rates} EXL3 "
+                               f"(BASELINE configs[{cfg_idx}])", "routing": args.routing,
                    "unique_experts_per_step": round(mean_uniq, 2),
                    "hidden": H, "inter": I, "experts": E, "shared": 1, "topk": TOPK, "tokens": T,
-                   "bits": args.bits, "layers_cycled": args.layers, "graph": graph is not None,
-                   "ksplit_gu": ws_ks(ws, 0), "ksplit_down": ws_ks(ws, 1)},
+                   "bits": None if prefill else args.bits, "layers_cycled": args.layers, "graph": graph is not None,
+                   "ksplit_gu": ws.shape.ksplit_gu, "ksplit_down": ws.shape.ksplit_down},
         "step_bytes": int(step_bytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
         "kernel_us": {k: round(v, 3) for k, v in kt.items()},
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline()
-    print(json.dumps(result), flush=True)
+        if prefill:
+            result["cpu_baseline"] = cpu_baseline(bits=4.0, tokens=16, n_routed=1)
+        else:
+            result["cpu_baseline"] = cpu_baseline(bits=args.bits, tokens=1, n_routed=1)
+    return result
+
+
+def run_stack(torch, args):
+    """an expert-only decode step through L stacked layers (all 257 x L experts
+    resident), 8 tokens, independent routing per layer, bf16 residual add between layers, the
+    whole step captured as one hipGraph (a copy of the step's input residual, then L layers)."""
+    from eva_amd import ops
+
+    dev = torch.device("cuda", 0)
+    T, L, K = args.tokens, args.layers, args.bits
+    layers = DeviceLayers(torch, dev, L, K, down_scale=STACK_DOWN_SCALE)
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    logits = torch.randn((L, T, E), generator=g, device=dev)
+    h0 = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    h = h0.clone()
+    ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
+                          ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down)
+    sels = torch.empty(L, T, TOPK, dtype=torch.int64, device=dev)
+    wts = torch.empty(L, T, TOPK, dtype=torch.float32, device=dev)
+
+    def layer(l, events=None):
+        ops.moe_forward(ws, h, layers.tables[l], None, limit=10.0, bits=K, logits=logits[l], sel=sels[l],
+                        weights=wts[l], shared_ptrs=layers.shared[l], shared_bits=K, residual=h, events=events)
+
+    def step():
+        h.copy_(h0)
+        for l in range(L):
+            layer(l)
+
+    step()
+    torch.cuda.synchronize()
+    if not torch.isfinite(h.float()).all():
+        raise RuntimeError("non-finite residual stream")
+    h_max = h.float().abs().max().item()
+    touched = [sorted(set(sels[l].reshape(-1).tolist())) for l in range(L)]
+    step_bytes = sum(layers.step_bytes(l, touched[l]) for l in range(L)) + L * (2 * T * H * 2 + T * E * 4)
+    mean_uniq = sum(len(t) for t in touched) / L
+
+    stream = torch.cuda.Stream(device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    steps = max(1, args.steps // 20)
+
+    def run_block(n):
+        with torch.cuda.stream(stream):
+            for _ in range(n):
+                graph.replay()
+
+    ms = timed_replays(torch, stream, run_block, steps, max(1, args.warmup // 20))
+    ms_step = ms / steps
+    gbps = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"{steps} graph replays of {L} layers: {ms_step:.3f} ms/step, {gbps:.1f} GB/s "
+        f"(unique experts/layer {mean_uniq:.1f})")
+    ref = h.clone()
+    run_block(1)
+    torch.cuda.synchronize()
+    if not torch.equal(ref, h):
+        raise RuntimeError("graph replays of the stacked step are not deterministic")
+
+    kt = kernel_times(torch, stream, lambda i, events=None: layer(i % L, events), L, skip=0)
+    gu_bytes_launch = sum(layers.gate_up_bytes(l, touched[l]) for l in range(L)) / L
+    roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, K))
+    result = {
+        "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "us_per_layer": round(ms_step * 1e3 / L, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5)/sqrt(H) svh, N(0,1) logits, bf16 N(0,1) h)",
+        "config": {"workload": f"DSv3 expert-only decode step, {L} stacked layers, {T} tokens, {K:g} bpw EXL3, "
+                               f"bf16 residual, one hipGraph (BASELINE configs[4])",
+                   "layers": L, "tokens": T, "bits": K, "resident_weight_gb": round(layers.trellis.numel() * 2 / 1e9, 2),
+                   "unique_experts_per_layer": round(mean_uniq, 2), "down_svh_scale": STACK_DOWN_SCALE,
+                   "residual_max_abs": round(h_max, 3), "hidden": H, "inter": I, "experts": E,
+                   "shared": 1, "topk": TOPK},
+        "step_bytes": int(step_bytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
+        "kernel_us": {k: round(v, 3) for k, v in kt.items()},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(bits=K, tokens=T, n_routed=1)
+    return result
+
+
+def gate_up_roofline(bytes_launch, us, traffic):
+    achieved = bytes_launch / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": "moe_gate_up", "achieved": round(achieved, 1), "peak": PEAK_HBM,
+            "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": int(bytes_launch), "avg_launch_us": round(us, 3)}
 
 
 COPY_BYTES = 1 << 30
@@ -297,37 +487,32 @@ def measured_traffic(tokens, bits):
         text = open(TRAFFIC_FILE).read()
     except OSError:
         return None
-    m = re.search(rf"^traffic_bytes_per_launch\[tokens={tokens},bits={bits:g}\]:\s*(\d+)", text, flags=re.M)
+    key = "mixed" if bits is None else f"{bits:g}"
+    m = re.search(rf"^traffic_bytes_per_launch\[tokens={tokens},bits={key}\]:\s*(\d+)", text, flags=re.M)
     return int(m.group(1)) if m else None
 
 
-def ws_ks(ws, which):
-    return ws.shape.ksplit_gu if which == 0 else ws.shape.ksplit_down
-
-
-def kernel_times(torch, ops, lib, ws, x, layers, logits, sel, wts, out, args, stream, n_draws, n=64):
+def kernel_times(torch, stream, step, n, skip):
     """Average duration of each of the five stages, from hipEvents recorded between the launches
-    on the launch stream (eager steps cycling the resident layers)."""
+    on the launch stream (eager calls step(i, events))."""
     names = ["moe_prepare", "moe_gate_up", "moe_act", "moe_down", "moe_combine"]
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(n)]
     for row in evs:
         for e in row:
             e.record(stream)          # creates the underlying hipEvent
+    torch.cuda.synchronize()
     handles = []
     with torch.cuda.stream(stream):
         for i in range(n):
-            l = i % args.layers
             hs = (ctypes.c_void_p * 6)(*[e.cuda_event for e in evs[i]])
             handles.append(hs)
-            ops.moe_forward(ws, x, layers.tables[l], out, limit=10.0, bits=args.bits, logits=logits[i % n_draws],
-                            sel=sel, weights=wts, shared_ptrs=layers.shared[l], shared_bits=args.bits,
-                            events=hs)
+            step(i, events=hs)
     torch.cuda.synchronize()
     acc = [0.0] * 5
-    for i in range(8, n):
+    for i in range(skip, n):
         for k in range(5):
             acc[k] += evs[i][k].elapsed_time(evs[i][k + 1])
-    return {names[k]: acc[k] * 1e3 / (n - 8) for k in range(5)}
+    return {names[k]: acc[k] * 1e3 / (n - skip) for k in range(5)}
 
 
 if __name__ == "__main__":

@@ -293,6 +293,8 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     EVAMX_REQUIRE(a->x && (a->out || a->residual) && a->tables && a->sel && a->workspace,
                   "evamx_moe_forward: null pointer");
     EVAMX_REQUIRE(a->x_dtype == EVAMX_DTYPE_F16 || a->x_dtype == EVAMX_DTYPE_BF16, "evamx_moe_forward: x_dtype %d", a->x_dtype);
+    EVAMX_REQUIRE(((uintptr_t)a->x & 3) == 0 && a->x_stride % 2 == 0,
+                  "evamx_moe_forward: x must be 4-byte aligned with an even row stride");
     EVAMX_REQUIRE(a->x_stride >= s->hidden && (!a->out || a->out_stride >= s->hidden) &&
                       (!a->residual || a->residual_stride >= s->hidden),
                   "evamx_moe_forward: row strides below hidden");

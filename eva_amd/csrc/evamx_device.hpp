@@ -181,8 +181,10 @@ __device__ __forceinline__ half2_t half_hpair(const uint32_t (&N)[B + 1])
 // reference for any data layout, because IEEE addition is commutative and each stage's
 // operand pairs are the same.
 
-// Value of lane (lane ^ M) for a compile-time M: DPP for M < 16 (quad permutes, row
-// rotations), an LDS-unit swizzle for 16 and a bpermute for 32.
+// Value of lane (lane ^ M) for a compile-time M, on the vector ALU only: DPP for M < 16 (quad
+// permutes, row rotations) and gfx950's row swaps for 16 and 32. permlane16_swap(v, v) gives
+// (rows 0,0,2,2 ; rows 1,1,3,3) of v, so lane ^ 16 reads the first for odd rows and the second
+// for even rows; permlane32_swap(v, v) gives (rows 0,1,0,1 ; rows 2,3,2,3) likewise.
 template <int M>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane)
 {
@@ -193,8 +195,14 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane)
         const uint32_t r12 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x12C, 0xf, 0xf, false);      // row_ror:12
         return (lane & 4) ? r4 : r12;
     } else if constexpr (M == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false); // row_ror:8
-    else if constexpr (M == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);           // xor 16 in 32
-    else return (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ M) << 2, (int)v);
+    else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        static_assert(M == 32, "lane xor 1, 2, 4, 8, 16 or 32");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? r[0] : r[1];
+    }
 }
 
 template <int M>

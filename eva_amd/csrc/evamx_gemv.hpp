@@ -37,6 +37,26 @@ __device__ __forceinline__ void had128_lane(float& v0, float& v1, int lane)
     v1 *= R_SCALE;
 }
 
+// The same transform for a chunk held as consecutive pairs, element e = 2*lane + h: stage 0 is
+// in-lane, stages 1..6 pair lanes xor 1..32. Same stage order and operand pairs as had128_lane,
+// so the results are bit-identical.
+__device__ __forceinline__ void had128_pair(float& v0, float& v1, int lane)
+{
+    {
+        const float a = v0, c = v1;
+        v0 = a + c;
+        v1 = a - c;
+    }
+    v0 = bfly_x<1>(v0, lane);  v1 = bfly_x<1>(v1, lane);
+    v0 = bfly_x<2>(v0, lane);  v1 = bfly_x<2>(v1, lane);
+    v0 = bfly_x<4>(v0, lane);  v1 = bfly_x<4>(v1, lane);
+    v0 = bfly_x<8>(v0, lane);  v1 = bfly_x<8>(v1, lane);
+    v0 = bfly_x<16>(v0, lane); v1 = bfly_x<16>(v1, lane);
+    v0 = bfly_x<32>(v0, lane); v1 = bfly_x<32>(v1, lane);
+    v0 *= R_SCALE;
+    v1 *= R_SCALE;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Streaming loads.
 
@@ -96,6 +116,76 @@ __device__ __forceinline__ void load_slice(LaneWords<K>& w, __amdgpu_buffer_rsrc
 }
 
 // ---------------------------------------------------------------------------------------------
+// Rate geometry and per-slice decode of the lane layout (lane = 8*i + q owns tile i's columns q
+// and q + 8 for the 16 k of a k-slice), shared by the decode GEMV and the MFMA path.
+
+// K2 = 2 x bits: even for integer rates (K = K2/2 words per lane), odd for rates b + 0.5.
+template <int K2>
+struct Rate {
+    static constexpr bool HALF = (K2 & 1) != 0;
+    static constexpr int B = K2 / 2;                          // whole bits (half rates)
+    static constexpr int K = HALF ? B + 1 : K2 / 2;           // words loaded per lane besides b[0]
+    static constexpr int TW = HALF ? 4 * (2 * B + 1) : 8 * K; // words per tile
+};
+
+// Byte offsets of a lane's words within its tile (lane_off: the K words, prev_off: the word
+// before them in the tile's circular bit string) and, at half rates, the normalising shift.
+template <int K2>
+__device__ __forceinline__ void lane_offsets(int lane, uint32_t& lane_off, uint32_t& prev_off, uint32_t& sh)
+{
+    using R = Rate<K2>;
+    const int q = lane & 7;
+    sh = 0;
+    if constexpr (!R::HALF) {
+        lane_off = 4u * (uint32_t)((lane >> 3) * R::TW + q * R::K);
+        prev_off = 4u * (uint32_t)((lane >> 3) * R::TW + (q == 0 ? R::TW - 1 : q * R::K - 1));
+    } else {
+        // words s0 .. s0+B+1 cover the lane's bits and the 16 before them; s0 = -1 (q = 0) wraps
+        // to the tile's last word, which is loaded on its own like the integer rates' b[0]
+        const int r0 = 16 * q * (2 * R::B + 1);
+        const int s0 = (r0 - 17 + 32) / 32 - 1;              // floor((r0 - 17) / 32)
+        lane_off = 4u * (uint32_t)((lane >> 3) * R::TW + s0 + 1);
+        prev_off = 4u * (uint32_t)((lane >> 3) * R::TW + (q == 0 ? R::TW - 1 : s0));
+        sh = (q & 1) ? 0u : 16u;
+    }
+}
+
+// The (1024 + bytesum) pairs of the lane's 32 positions of one k-slice:
+// wp[4u + 2c + kh] = column q + 8c, k = 8kh + 2u and 8kh + 2u + 1 (low half: even k).
+template <int K2>
+__device__ __forceinline__ void decode_slice(const LaneWords<Rate<K2>::K>& w, uint32_t sh, half2_t (&wp)[16])
+{
+    using R = Rate<K2>;
+    constexpr int K = R::K, B = R::B;
+    if constexpr (!R::HALF) {
+#define EVAMX_DEC_UNIT(U)                                \
+        wp[4 * U + 0] = lane_hpair<K, 8 * U + 0>(w);     \
+        wp[4 * U + 1] = lane_hpair<K, 8 * U + 2>(w);     \
+        wp[4 * U + 2] = lane_hpair<K, 8 * U + 4>(w);     \
+        wp[4 * U + 3] = lane_hpair<K, 8 * U + 6>(w);
+        EVAMX_DEC_UNIT(0)
+        EVAMX_DEC_UNIT(1)
+        EVAMX_DEC_UNIT(2)
+        EVAMX_DEC_UNIT(3)
+#undef EVAMX_DEC_UNIT
+    } else {
+        uint32_t N[B + 1];
+#pragma unroll
+        for (int k = 0; k <= B; ++k) N[k] = __builtin_amdgcn_alignbit(w.b[k], w.b[k + 1], sh);
+#define EVAMX_DEC_UNIT(U)                                \
+        wp[4 * U + 0] = half_hpair<B, 8 * U + 0>(N);     \
+        wp[4 * U + 1] = half_hpair<B, 8 * U + 2>(N);     \
+        wp[4 * U + 2] = half_hpair<B, 8 * U + 4>(N);     \
+        wp[4 * U + 3] = half_hpair<B, 8 * U + 6>(N);
+        EVAMX_DEC_UNIT(0)
+        EVAMX_DEC_UNIT(1)
+        EVAMX_DEC_UNIT(2)
+        EVAMX_DEC_UNIT(3)
+#undef EVAMX_DEC_UNIT
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Activation rows of a GEMV chunk: row m holds the k-vector of slot slot_of[m], read through
 // wave-uniform addresses (scalar loads), together with its per-128-chunk sums (fp32) that the
 // affine codebook map needs.
@@ -116,18 +206,15 @@ struct GlobalRows {
 template <int TM>
 constexpr int prefetch_depth() { return TM <= 2 ? 7 : 4; }
 
-// K2 = 2 x bits: even for integer rates (K = K2/2 words per lane), odd for rates b + 0.5.
 template <int K2, int TM>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
                                           const GlobalRows& src, const uint32_t (&aoff)[TM], int tm, float (&acc)[TM][2])
 {
-    constexpr bool HALF = (K2 & 1) != 0;
-    constexpr int B = K2 / 2;                                // whole bits (half rates)
-    constexpr int K = HALF ? B + 1 : K2 / 2;                 // words loaded per lane besides b[0]
-    constexpr int TW = HALF ? 4 * (2 * B + 1) : 8 * K;       // words per tile
+    using R = Rate<K2>;
+    constexpr int K = R::K;
+    constexpr int TW = R::TW;
     constexpr int PF = prefetch_depth<TM>();
     const int lane = threadIdx.x & 63;
-    const int q = lane & 7;
     // the k-range is wave-uniform: keep it (and all index math below) in scalar registers
     kt0 = __builtin_amdgcn_readfirstlane(kt0);
     kt1 = __builtin_amdgcn_readfirstlane(kt1);
@@ -136,20 +223,8 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
     const uint32_t slice = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(nt_n * TW));
     const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW));
     const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(trellis);
-    uint32_t lane_off, prev_off;
-    uint32_t sh = 0;                                         // half rates: normalising shift
-    if constexpr (!HALF) {
-        lane_off = 4u * (uint32_t)((lane >> 3) * TW + q * K);
-        prev_off = 4u * (uint32_t)((lane >> 3) * TW + (q == 0 ? TW - 1 : q * K - 1));
-    } else {
-        // words s0 .. s0+B+1 cover the lane's bits and the 16 before them; s0 = -1 (q = 0) wraps
-        // to the tile's last word, which is loaded on its own like the integer rates' b[0]
-        const int r0 = 16 * q * (2 * B + 1);
-        const int s0 = (r0 - 17 + 32) / 32 - 1;              // floor((r0 - 17) / 32)
-        lane_off = 4u * (uint32_t)((lane >> 3) * TW + s0 + 1);
-        prev_off = 4u * (uint32_t)((lane >> 3) * TW + (q == 0 ? TW - 1 : s0));
-        sh = (q & 1) ? 0u : 16u;
-    }
+    uint32_t lane_off, prev_off, sh;
+    lane_offsets<K2>(lane, lane_off, prev_off, sh);
 
 #pragma unroll
     for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = 0.0f;
@@ -184,32 +259,7 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
         half2_t xn[TM][8];
         if constexpr (XPF) load_x(xn, min(kt + 1, last));
         half2_t wp[16];
-        if constexpr (!HALF) {
-#define EVAMX_DEC_UNIT(U)                                \
-            wp[4 * U + 0] = lane_hpair<K, 8 * U + 0>(w); \
-            wp[4 * U + 1] = lane_hpair<K, 8 * U + 2>(w); \
-            wp[4 * U + 2] = lane_hpair<K, 8 * U + 4>(w); \
-            wp[4 * U + 3] = lane_hpair<K, 8 * U + 6>(w);
-            EVAMX_DEC_UNIT(0)
-            EVAMX_DEC_UNIT(1)
-            EVAMX_DEC_UNIT(2)
-            EVAMX_DEC_UNIT(3)
-#undef EVAMX_DEC_UNIT
-        } else {
-            uint32_t N[B + 1];
-#pragma unroll
-            for (int k = 0; k <= B; ++k) N[k] = __builtin_amdgcn_alignbit(w.b[k], w.b[k + 1], sh);
-#define EVAMX_DEC_UNIT(U)                                \
-            wp[4 * U + 0] = half_hpair<B, 8 * U + 0>(N); \
-            wp[4 * U + 1] = half_hpair<B, 8 * U + 2>(N); \
-            wp[4 * U + 2] = half_hpair<B, 8 * U + 4>(N); \
-            wp[4 * U + 3] = half_hpair<B, 8 * U + 6>(N);
-            EVAMX_DEC_UNIT(0)
-            EVAMX_DEC_UNIT(1)
-            EVAMX_DEC_UNIT(2)
-            EVAMX_DEC_UNIT(3)
-#undef EVAMX_DEC_UNIT
-        }
+        decode_slice<K2>(w, sh, wp);
         load_slice<K>(w, rsrc, cbase + (uint32_t)min(kt + PF, last) * slice, lane_off, prev_off);
 #pragma unroll
         for (int m = 0; m < TM; ++m) {

@@ -10,6 +10,7 @@ namespace evamx {
 constexpr int EVAMX_MAX_EXPERTS = 512;     // pointer-table entries per layer (reference: <= 384)
 constexpr int EVAMX_MAX_TOPK = 32;         // reference bound: top_k <= 32 (exl3_moe_coop_kernel.cuh:46)
 constexpr int EVAMX_CHUNK = 8;             // slots of one expert per GEMV work item
+constexpr int EVAMX_TILE_ROWS = 64;        // slots of one expert per MFMA work item
 
 // Pointer-table rows, in the reference's order (ds41/cache.py:1877-1886).
 enum {
@@ -22,6 +23,8 @@ enum { PREP_GROUP = 1, PREP_MOE = 2 };
 
 struct MoeParams {
     int mode;
+    int mfma;                  // 1: expert GEMMs on the MFMA path (tiles of EVAMX_TILE_ROWS, one k-split)
+    int chunk_rows;            // rows per GEMV chunk / MFMA tile (0: EVAMX_CHUNK)
     int T, H, I, topk, n_local, n_logits;
     // input rows
     const void* x;
@@ -114,15 +117,20 @@ __device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
 
 __device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
 {
+    if (p.mfma) return KSplit{1, 1};
     return moe_ksplit(p.ks_gu, units * 2 * (p.I / 128), p.gemv_waves, p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
 }
 
 __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
 {
+    if (p.mfma) return KSplit{1, 1};
     return moe_ksplit(p.ks_d, units * (p.H / 128), p.gemv_waves, p.ks_d_max, p.cap_rows_d, moe_nslot(p));
 }
 
+__host__ __device__ __forceinline__ int chunk_rows_of(const MoeParams& p) { return p.chunk_rows > 0 ? p.chunk_rows : EVAMX_CHUNK; }
+
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);
+int launch_mfma(const MoeParams& p, int which, hipStream_t stream);
 int moe_prepare_only(MoeParams& p, hipStream_t stream);
 bool moe_small_path(int T, int topk);
 

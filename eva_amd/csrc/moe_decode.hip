@@ -98,9 +98,7 @@ __device__ __forceinline__ half_t load_x16(const void* x, int dtype, size_t i)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Routing of one token by one wave: top-k by (key desc, index asc); weights from the scores.
-// Lane j < topk writes slot j to sel_o / rw_o and, when publishing, to the global outputs.
-// Keys are packed as (order-preserving key bits << 32 | ~index) so that one 64-bit max, reduced
+// Router keys are packed as (order-preserving key bits << 32 | ~index) so that one 64-bit max, reduced
 // with lane butterflies, yields the winner and the tie rule at once (+0 and -0 compare equal).
 
 __device__ __forceinline__ uint64_t pack_key(float k, int e)
@@ -120,9 +118,9 @@ __device__ __forceinline__ uint64_t max_x(uint64_t v, int lane)
     return p > v ? p : v;
 }
 
-__device__ void route_token(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
+template <int NPER>
+__device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
 {
-    constexpr int NPER = EVAMX_MAX_EXPERTS / 64;
     const float* z = p.logits + (size_t)r * p.n_logits;
     float zr[NPER];
     uint64_t key[NPER];
@@ -142,7 +140,8 @@ __device__ void route_token(const MoeParams& p, int r, int lane, int* sel_o, hal
         }
         key[i] = e < p.n_logits ? pack_key(k, e) : 0ull;
     }
-    float tot = 0.0f, my_score = 0.0f;
+    // winners one at a time; lane j keeps winner j's index and logit
+    float my_z = 0.0f;
     int my_id = 0;
     for (int j = 0; j < p.topk; ++j) {
         uint64_t best = 0ull;
@@ -163,13 +162,16 @@ __device__ void route_token(const MoeParams& p, int r, int lane, int* sel_o, hal
                 mine = zr[i];
             }
         }
-        const float sc = score_fn(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), bi & 63)),
-                                  p.score);
-        tot = tot + sc;
-        if (lane == j) { my_score = sc; my_id = bi; }
+        const float zb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), bi & 63));
+        if (lane == j) { my_z = zb; my_id = bi; }
     }
+    // scores of the winners in parallel, their total in slot order
+    const float sc = lane < p.topk ? score_fn(my_z, p.score) : 0.0f;
+    float tot = 0.0f;
+    for (int j = 0; j < p.topk; ++j)
+        tot = tot + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), j));
     if (lane < p.topk) {
-        const float w = route_weight(my_score, tot, p.route_scale);
+        const float w = route_weight(sc, tot, p.route_scale);
         const int s = r * p.topk + lane;
         if (sel_o) sel_o[s] = my_id;
         if (rw_o) rw_o[s] = f2h(w);
@@ -179,6 +181,14 @@ __device__ void route_token(const MoeParams& p, int r, int lane, int* sel_o, hal
             p.rw16[s] = f2h(w);
         }
     }
+}
+
+// Routing of one token by one wave: top-k by (key desc, index asc); weights from the scores.
+// Lane j < topk writes slot j to sel_o / rw_o and, when publishing, to the global outputs.
+__device__ __forceinline__ void route_token(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
+{
+    if (p.n_logits <= 256) route_token_n<4>(p, r, lane, sel_o, rw_o, publish);
+    else route_token_n<EVAMX_MAX_EXPERTS / 64>(p, r, lane, sel_o, rw_o, publish);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -201,28 +211,47 @@ __device__ __forceinline__ int expert_units(int n)
     return full * chunk_mult(EVAMX_CHUNK) + (rest ? chunk_mult(rest) : 0);
 }
 
-// Exclusive scan of a[0..n) in place by one wave, a[n] = total (n <= 1024).
-__device__ void wave_excl_scan(int* a, int n, int lane)
+// Inclusive scan over the wave of one int per lane, on the vector ALU: row-local DPP shifts
+// (row_shr 1, 2, 4, 8, zero fill), then the row totals carried forward (row_bcast:15 into
+// rows 1 and 3, row_bcast:31 into rows 2 and 3).
+__device__ __forceinline__ int wave_incl_scan(int v)
 {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+    return v;
+}
+
+// Exclusive scans of four arrays a[k][0..n) in place by one wave, a[k][n] = total (n <= 1024):
+// each lane owns a contiguous block of every array, and the four lane-total scans run together.
+__device__ void wave_excl_scan4(int* a0, int* a1, int* a2, int* a3, int n, int lane)
+{
+    int* const a[4] = {a0, a1, a2, a3};
     const int per = (n + 63) / 64;
     const int b0 = lane * per;
-    int sum = 0;
-    for (int i = 0; i < per; ++i)
-        if (b0 + i < n) sum += a[b0 + i];
-    int incl = sum;
+    int sum[4], run[4];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(incl, o, WAVE);
-        if (lane >= o) incl += v;
+    for (int k = 0; k < 4; ++k) {
+        sum[k] = 0;
+        for (int i = 0; i < per; ++i)
+            if (b0 + i < n) sum[k] += a[k][b0 + i];
     }
-    int run = incl - sum;
-    for (int i = 0; i < per; ++i)
-        if (b0 + i < n) {
-            const int v = a[b0 + i];
-            a[b0 + i] = run;
-            run += v;
-        }
-    if (lane == 63) a[n] = incl;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) run[k] = wave_incl_scan(sum[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int r = run[k] - sum[k];
+        for (int i = 0; i < per; ++i)
+            if (b0 + i < n) {
+                const int v = a[k][b0 + i];
+                a[k][b0 + i] = r;
+                r += v;
+            }
+        if (lane == 63) a[k][n] = run[k];
+    }
 }
 
 // Slot activity (exl3_moe_coop_kernel.cuh:208-223) -> local[s] = local expert or -1 (bounds
@@ -261,13 +290,10 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
         for (int e = lane; e < E; e += 64) {
             ex.off[e] = ex.cnt[e];
             ex.run_base[e] = (ex.cnt[e] + 7) / 8;
-            ex.chunk_base[e] = (ex.cnt[e] + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
+            ex.chunk_base[e] = (ex.cnt[e] + chunk_rows_of(p) - 1) / chunk_rows_of(p);
             ex.unit_base[e] = expert_units(ex.cnt[e]);
         }
-        wave_excl_scan(ex.off, E, lane);
-        wave_excl_scan(ex.run_base, E, lane);
-        wave_excl_scan(ex.chunk_base, E, lane);
-        wave_excl_scan(ex.unit_base, E, lane);
+        wave_excl_scan4(ex.off, ex.run_base, ex.chunk_base, ex.unit_base, E, lane);
         // Stable scatter by (expert, slot): blocks of 64 slots in order; lanes holding the same
         // expert find each other with one ballot per expert-index bit.
         for (int s0 = 0; s0 < slots; s0 += 64) {
@@ -300,23 +326,25 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
     __syncthreads();
 }
 
-// Chunks of <= EVAMX_CHUNK slots per expert, then the shared expert's rows; their work units
-// (unit -> chunk map) and each slot's chunk weight. `order` is the grouped slot order.
+// Chunks of <= chunk_rows_of(p) slots per expert, then the shared expert's rows; for the decode
+// GEMV also their work units (unit -> chunk map) and each slot's chunk weight. `order` is the
+// grouped slot order.
 __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int* order)
 {
     const int t = threadIdx.x, nt = blockDim.x;
     const int E = p.n_local;
+    const int CR = chunk_rows_of(p);
     const int n_active = ex.off[E];
     for (int e = t; e < E; e += nt) {
         const int n = ex.cnt[e];
         int u = ex.unit_base[e];
-        for (int j = 0; j * EVAMX_CHUNK < n; ++j) {
+        for (int j = 0; j * CR < n; ++j) {
             const int ci = ex.chunk_base[e] + j;
-            const int rows = min(EVAMX_CHUNK, n - j * EVAMX_CHUNK);
+            const int rows = min(CR, n - j * CR);
             const int m = chunk_mult(rows);
             int* c = p.chunks + 8 * ci;
             c[0] = e;
-            c[1] = ex.off[e] + j * EVAMX_CHUNK;
+            c[1] = ex.off[e] + j * CR;
             c[2] = rows;
             c[3] = p.k2_per_expert ? (int)p.k2_per_expert[e] : p.k2_uniform;
             if (!gemv_k2_supported(c[3]) && j == 0) atomicOr(p.err, EVAMX_ERR_RATE);
@@ -324,37 +352,41 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             c[5] = m;
             c[6] = 0;
             c[7] = 0;
-            for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
-            for (int i = 0; i < rows; ++i) p.slot_mult[order[c[1] + i]] = m;
+            if (!p.mfma) {
+                for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
+                for (int i = 0; i < rows; ++i) p.slot_mult[order[c[1] + i]] = m;
+            }
             u += m;
         }
     }
     if (p.has_shared) {
         const int base = ex.chunk_base[E];
-        const int nsc = (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
+        const int nsc = (p.T + CR - 1) / CR;
         const int slots = p.T * p.topk;
         for (int j = t; j < nsc; j += nt) {
-            const int rows = min(EVAMX_CHUNK, p.T - j * EVAMX_CHUNK);
+            const int rows = min(CR, p.T - j * CR);
             const int m = chunk_mult(rows);
-            const int u = ex.unit_base[E] + j * chunk_mult(EVAMX_CHUNK);     // earlier chunks are full
+            const int u = ex.unit_base[E] + j * chunk_mult(CR);     // earlier chunks are full
             int* c = p.chunks + 8 * (base + j);
             c[0] = -1;
-            c[1] = n_active + j * EVAMX_CHUNK;
+            c[1] = n_active + j * CR;
             c[2] = rows;
             c[3] = p.k2_shared;
             c[4] = u;
             c[5] = m;
             c[6] = 0;
             c[7] = 0;
-            for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
-            for (int i = 0; i < rows; ++i) p.slot_mult[slots + j * EVAMX_CHUNK + i] = m;
+            if (!p.mfma) {
+                for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
+                for (int i = 0; i < rows; ++i) p.slot_mult[slots + j * CR + i] = m;
+            }
         }
     }
 }
 
 __device__ __forceinline__ int total_chunks(const MoeParams& p, const ExpertLds& ex)
 {
-    return ex.chunk_base[p.n_local] + (p.has_shared ? (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
+    return ex.chunk_base[p.n_local] + (p.has_shared ? (p.T + chunk_rows_of(p) - 1) / chunk_rows_of(p) : 0);
 }
 
 __device__ __forceinline__ int total_units(const MoeParams& p, const ExpertLds& ex)
@@ -363,32 +395,82 @@ __device__ __forceinline__ int total_units(const MoeParams& p, const ExpertLds& 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Input rotation of one (slot, 128-chunk, gate|up) item by one wave.
+// Input rotations fp16(H128(x * suh)) of the grouped rows, with their 128-chunk sums. Work is
+// cut into units (grouped row o, gate|up) of H/128 chunks, and each unit into `parts` equal
+// chunk ranges so that the waves of the grid have one range each (grid-stride beyond that).
+// A wave resolves its row's slot, expert and suh pointer once, then works through its chunks
+// in batches whose x and suh loads are all issued before the first butterfly.
 
-__device__ void rotate_item(const MoeParams& p, int s, int e, int c, int proj, int lane)
+constexpr int ROT_BATCH = 8;
+
+__device__ __forceinline__ float x_elem(uint32_t w, int hi, int dtype)
+{
+    if (dtype == EVAMX_DTYPE_F16) {
+        const half2_t h = __builtin_bit_cast(half2_t, w);
+        return h2f(hi ? h.y : h.x);
+    }
+    return __builtin_bit_cast(float, hi ? (w & 0xffff0000u) : (w << 16));
+}
+
+// Chunks [c0, c1) of grouped slot s (routed slot < T*topk with local expert e, or shared row).
+__device__ void rotate_chunks(const MoeParams& p, int s, int e, int proj, int c0, int c1, int lane)
 {
     const int slots = p.T * p.topk;
     const bool shared = s >= slots;
     const int row = shared ? s - slots : s / p.topk;
     const int trow = proj == 0 ? EVAMX_TBL_G_SUH : EVAMX_TBL_U_SUH;
     const half_t* suh = shared ? (const half_t*)p.sh_ptr[trow] : (const half_t*)p.tables[(size_t)trow * p.tbl_stride + e];
-    float v[2];
+    const uint32_t* xw = (const uint32_t*)((const uint16_t*)p.x + (size_t)row * p.x_stride) + lane;
+    const uint32_t* sw = (const uint32_t*)suh + lane;
+    uint32_t* dst = (uint32_t*)(p.xr + ((size_t)proj * p.nslot_max + s) * p.H) + lane;
+    float* sums = p.xsum + ((size_t)proj * p.nslot_max + s) * (p.H / 128);
+    for (int b = c0; b < c1; b += ROT_BATCH) {
+        uint32_t xv[ROT_BATCH], sv[ROT_BATCH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int col = c * 128 + lane_col(lane, h);
-        const half_t xv = load_x16(p.x, p.x_dtype, (size_t)row * p.x_stride + col);
-        const half_t sv = suh[col];
-        // routed: fp32 product (exl3_moe_coop_kernel.cuh:186-191); shared EXL3 linear: fp16
-        // product (hadamard_inner.cuh:109-115)
-        v[h] = shared ? h2f(f2h(h2f(xv) * h2f(sv))) : h2f(xv) * h2f(sv);
+        for (int j = 0; j < ROT_BATCH; ++j) {
+            if (b + j < c1) {
+                xv[j] = xw[(b + j) * 64];
+                sv[j] = sw[(b + j) * 64];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < ROT_BATCH; ++j) {
+            if (b + j < c1) {
+                const half2_t su = __builtin_bit_cast(half2_t, sv[j]);
+                float v0 = x_elem(xv[j], 0, p.x_dtype) * h2f(su.x);
+                float v1 = x_elem(xv[j], 1, p.x_dtype) * h2f(su.y);
+                if (shared) {
+                    // shared EXL3 linear: fp16 product (hadamard_inner.cuh:109-115); routed
+                    // experts: fp32 product (exl3_moe_coop_kernel.cuh:186-191)
+                    v0 = h2f(f2h(h2f(f2h(x_elem(xv[j], 0, p.x_dtype))) * h2f(su.x)));
+                    v1 = h2f(f2h(h2f(f2h(x_elem(xv[j], 1, p.x_dtype))) * h2f(su.y)));
+                }
+                had128_pair(v0, v1, lane);
+                const half2_t r = {f2h(v0), f2h(v1)};
+                dst[(b + j) * 64] = __builtin_bit_cast(uint32_t, r);
+                const float sum = wave_sum(h2f(r.x) + h2f(r.y));
+                if (lane == 0) sums[b + j] = sum;
+            }
+        }
     }
-    had128_lane(v[0], v[1], lane);
-    half_t* dst = p.xr + ((size_t)proj * p.nslot_max + s) * p.H + c * 128;
-    const half_t r0 = f2h(v[0]), r1 = f2h(v[1]);
-    dst[lane_col(lane, 0)] = r0;
-    dst[lane_col(lane, 1)] = r1;
-    const float sum = wave_sum(h2f(r0) + h2f(r1));
-    if (lane == 0) p.xsum[((size_t)proj * p.nslot_max + s) * (p.H / 128) + c] = sum;
+}
+
+// Rotations of n_rows grouped rows by the waves [w0, w0 + nw) of the grid.
+__device__ void rotate_rows(const MoeParams& p, const int* order, const int* local, int n_rows, int w, int nw, int lane)
+{
+    const int nch = p.H / 128;
+    const int units = n_rows * 2;
+    if (units == 0) return;
+    int parts = nw / units;
+    parts = parts < 1 ? 1 : (parts > nch ? nch : parts);
+    const int slots = p.T * p.topk;
+    for (int it = w; it < units * parts; it += nw) {
+        const int u = it / parts, part = it - u * parts;
+        const int o = u >> 1, proj = u & 1;
+        const int s = __builtin_amdgcn_readfirstlane(order[o]);
+        const int e = s < slots ? __builtin_amdgcn_readfirstlane(local[s]) : -1;
+        rotate_chunks(p, s, e, proj, nch * part / parts, nch * (part + 1) / parts, lane);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -446,33 +528,27 @@ __global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
             p.meta[2] = total_units(p, sh.ex);
         }
     }
-    // rotations: items (o, chunk, proj) over the grouped order, grid-stride by wave
-    const int nch = p.H / 128;
-    const int n_items = (n_active + (p.has_shared ? p.T : 0)) * nch * 2;
-    for (int it = blockIdx.x * 4 + wave; it < n_items; it += gridDim.x * 4) {
-        const int o = it / (nch * 2);
-        const int rem = it % (nch * 2);
-        const int s = sh.order[o];
-        rotate_item(p, s, s < slots ? sh.local[s] : -1, rem >> 1, rem & 1, lane);
-    }
+    rotate_rows(p, sh.order, sh.local, n_active + (p.has_shared ? p.T : 0), blockIdx.x * 4 + wave, gridDim.x * 4, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
-// Prepare for any batch: one workgroup of 1024 threads with the per-slot arrays in global
-// memory. Mode bits select routing only, routing + run table, or the whole MoE prologue except
-// the rotation (moe_rotate_kernel follows).
+// Prepare for any batch, in three launches: routing (one wave per token), grouping (one
+// workgroup of 1024 threads, per-slot arrays in global memory), rotations (a full grid).
 
-__global__ __launch_bounds__(1024) void moe_prepare_large_kernel(MoeParams p)
+__global__ __launch_bounds__(256) void moe_route_kernel(MoeParams p)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6));
+    if (r < p.T) route_token(p, r, lane, nullptr, nullptr, true);
+}
+
+__global__ __launch_bounds__(1024) void moe_group_kernel(MoeParams p)
 {
     __shared__ ExpertLds ex;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x;
     const int slots = p.T * p.topk;
-    if (p.logits) {
-        for (int r = wave; r < p.T; r += 16) route_token(p, r, lane, nullptr, nullptr, true);
-    } else if (p.weights) {
+    if (!p.logits && p.weights)
         for (int s = t; s < slots; s += 1024) p.rw16[s] = f2h(p.weights[s]);
-    }
-    if (!(p.mode & PREP_GROUP)) return;
     if (p.runs) {
         const int table_len = 2 + 2 * p.slots_max + 1;
         for (int i = t; i < table_len; i += 1024) p.runs[i] = 0;
@@ -497,19 +573,13 @@ __global__ __launch_bounds__(1024) void moe_prepare_large_kernel(MoeParams p)
     }
 }
 
+constexpr int EVAMX_ROTATE_BLOCKS = 2048;
+
 __global__ __launch_bounds__(256) void moe_rotate_kernel(MoeParams p)
 {
     const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int nch = p.H / 128;
-    const int slots = p.T * p.topk;
-    const int n_rows = p.meta[1] + (p.has_shared ? p.T : 0);
-    for (int it = wid; it < n_rows * nch * 2; it += gridDim.x * 4) {
-        const int o = it / (nch * 2);
-        const int rem = it % (nch * 2);
-        const int s = p.order[o];
-        rotate_item(p, s, s < slots ? p.local[s] : -1, rem >> 1, rem & 1, lane);
-    }
+    const int w = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6));
+    rotate_rows(p, p.order, p.local, p.meta[1] + (p.has_shared ? p.T : 0), w, gridDim.x * 4, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -580,8 +650,9 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const half_t* u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
     const half_t* d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
     const float L = p.limit;
-    const int Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
-                               __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
+    // the MFMA path writes one split and no chunk weights
+    const int Sg = p.mfma ? 1 : ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
+                                            __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
     const int nslot = moe_nslot(p);
     float g[2], u[2];
 #pragma unroll
@@ -703,36 +774,41 @@ __device__ __forceinline__ void sum_partials(const MoeParams& p, int s, int cg, 
     }
 }
 
-// Per-token reduction over slots in slot order (+ shared expert). One workgroup of 4 waves per
-// (token, 128 columns): wave w handles slots w, w+4, ... (output rotation * svh * weight) into
-// LDS, then wave 0 sums them in slot order, as the reference sums one warp per slot
-// (exl3_moe_coop_kernel.cuh:906-940), and adds the shared expert.
-__global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
+// Per-token reduction over slots in slot order (+ shared expert). One workgroup per (token,
+// 128 columns) with one wave per item (slot or shared expert; grid-stride when there are more
+// items than waves): output rotation * svh * weight into LDS, then wave 0 sums them in slot
+// order, as the reference sums one warp per slot (exl3_moe_coop_kernel.cuh:906-940), and adds
+// the shared expert. A wave issues its item's independent loads (expert, weight, split count)
+// together, then the svh pointer and the partials, so an item costs two memory round trips.
+constexpr int EVAMX_COMBINE_WAVES = 16;
+
+__global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(MoeParams p)
 {
     __shared__ float part[EVAMX_MAX_TOPK + 1][128];
     __shared__ int active[EVAMX_MAX_TOPK + 1];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int ncg = p.H / 128;
     const int row = blockIdx.x / ncg, cg = blockIdx.x % ncg;
     const int slots = p.T * p.topk;
-    const KSplit kd = ks_down(p, __builtin_amdgcn_readfirstlane(p.meta[2]));
     const int c0 = lane_col(lane, 0), c1 = lane_col(lane, 1);
     const int col0 = cg * 128 + c0, col1 = cg * 128 + c1;
     const int nitems = p.topk + (p.has_shared ? 1 : 0);
-    for (int k = wave; k < nitems; k += 4) {
+    for (int k = wave; k < nitems; k += nw) {
         const bool shared = k == p.topk;
         const int sk = shared ? slots + row : row * p.topk + k;
-        const int le = shared ? -1 : p.local[sk];
+        const int le = shared ? -1 : __builtin_amdgcn_readfirstlane(p.local[sk]);
+        const int mult = __builtin_amdgcn_readfirstlane(p.slot_mult[sk]);
+        const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
+        const float w = shared ? 1.0f : h2f(p.rw16[sk]);
         if (!shared && le < 0) {
             if (lane == 0) active[k] = 0;
             continue;
         }
         const half_t* svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
                                    : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
-        const float w = shared ? 1.0f : h2f(p.rw16[sk]);
-        const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
         float v[2];
-        sum_partials(p, sk, cg, lane, ks_of_chunk(kd, p.slot_mult[sk]), v);
+        sum_partials(p, sk, cg, lane, p.mfma ? 1 : ks_of_chunk(ks_down(p, units), mult), v);
+        const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
         if (shared) {
             v[0] = h2f(f2h(v[0]));                     // EXL3 linear C in fp16
             v[1] = h2f(f2h(v[1]));
@@ -778,7 +854,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p)
 
 int moe_prepare_only(MoeParams& p, hipStream_t stream)
 {
-    hipLaunchKernelGGL(moe_prepare_large_kernel, dim3(1), dim3(1024), 0, stream, p);
+    if (p.logits) hipLaunchKernelGGL(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
+    if (p.mode & PREP_GROUP) hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -791,32 +868,43 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     };
     const int nch = p.H / 128;
     const int nslot = p.T * p.topk + (p.has_shared ? p.T : 0);
+    const bool small = moe_small_path(p.T, p.topk);
+    p.mfma = small ? 0 : 1;
+    p.chunk_rows = small ? EVAMX_CHUNK : EVAMX_TILE_ROWS;
     mark(0);
-    if (moe_small_path(p.T, p.topk)) {
+    if (small) {
         int blocks = (nslot * nch * 2 + 3) / 4;
         if (blocks > 256) blocks = 256;
         hipLaunchKernelGGL(moe_prepare_small_kernel, dim3(blocks), dim3(256), 0, stream, p);
     } else {
-        hipLaunchKernelGGL(moe_prepare_large_kernel, dim3(1), dim3(1024), 0, stream, p);
-        hipLaunchKernelGGL(moe_rotate_kernel, dim3(256), dim3(256), 0, stream, p);
+        if (p.logits) hipLaunchKernelGGL(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, p);
+        hipLaunchKernelGGL(moe_rotate_kernel, dim3(EVAMX_ROTATE_BLOCKS), dim3(256), 0, stream, p);
     }
     mark(1);
-    // Chunks hold at most min(T, EVAMX_CHUNK) rows: each token picks an expert once, and the
-    // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
-    const int tmax = tmax_for(p.T < EVAMX_CHUNK ? p.T : EVAMX_CHUNK);
-    {
-        const int units = EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128);
-        const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
-        const half_t* xr = p.xr;
-        switch (tmax) {
-            case 1: hipLaunchKernelGGL(moe_gate_up_kernel<1>, grid, dim3(256), 0, stream, p, xr); break;
-            case 2: hipLaunchKernelGGL(moe_gate_up_kernel<2>, grid, dim3(256), 0, stream, p, xr); break;
-            case 4: hipLaunchKernelGGL(moe_gate_up_kernel<4>, grid, dim3(256), 0, stream, p, xr); break;
-            default: hipLaunchKernelGGL(moe_gate_up_kernel<8>, grid, dim3(256), 0, stream, p, xr); break;
+    if (p.mfma) {
+        launch_mfma(p, 0, stream);
+        mark(2);
+        const int waves = nslot * (p.I / 128);
+        hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        mark(3);
+        launch_mfma(p, 1, stream);
+    } else {
+        // Chunks hold at most min(T, EVAMX_CHUNK) rows: each token picks an expert once, and the
+        // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
+        const int tmax = tmax_for(p.T < EVAMX_CHUNK ? p.T : EVAMX_CHUNK);
+        {
+            const int units = EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128);
+            const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
+            const half_t* xr = p.xr;
+            switch (tmax) {
+                case 1: hipLaunchKernelGGL(moe_gate_up_kernel<1>, grid, dim3(256), 0, stream, p, xr); break;
+                case 2: hipLaunchKernelGGL(moe_gate_up_kernel<2>, grid, dim3(256), 0, stream, p, xr); break;
+                case 4: hipLaunchKernelGGL(moe_gate_up_kernel<4>, grid, dim3(256), 0, stream, p, xr); break;
+                default: hipLaunchKernelGGL(moe_gate_up_kernel<8>, grid, dim3(256), 0, stream, p, xr); break;
+            }
         }
-    }
-    mark(2);
-    {
+        mark(2);
         const int waves = nslot * (p.I / 128);
         hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
         mark(3);
@@ -831,7 +919,11 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         }
     }
     mark(4);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(256), 0, stream, p);
+    {
+        int nw = p.topk + (p.has_shared ? 1 : 0);
+        if (nw > EVAMX_COMBINE_WAVES) nw = EVAMX_COMBINE_WAVES;
+        hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(64 * nw), 0, stream, p);
+    }
     mark(5);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -1,0 +1,271 @@
+// Prefill-shaped expert GEMMs on gfx950: trellis decode into LDS feeding fp16 MFMA.
+//
+// Replaces the reference's grouped expert matmuls for large batches (the coop kernels'
+// gemv_tile, exl3_moe_coop_kernel.cuh:340-544, run once per <= 8-row run). Here a work item is
+// (tile of <= 64 grouped rows of one expert, 128 output columns, projection), one wave each,
+// over the full k range, so every weight is decoded once per 64 rows instead of once per 8:
+//
+//   - the wave streams its 8 trellis tiles per k-slice exactly like the decode GEMV (lane
+//     8*i + q owns tile i's columns q, q + 8) and decodes two k-slices into the (1024 +
+//     bytesum) fp16 values of the affine codebook map (w = 0x1eee * h + 0xc931);
+//   - it restages them through a wave-private 8 KiB LDS region into the B operands of
+//     v_mfma_f32_16x16x32_f16 (lane n + 16 g holds column n, k = 8g .. 8g+7), one per 16-column
+//     tile, and reads the rotated activations of its rows as the A operands (lane m + 16 g
+//     holds row m, the same k) straight from global memory;
+//   - 4 x 8 accumulators (64 rows x 128 columns, fp32) take sum_k x_k h_k, and the epilogue
+//     applies the codebook map per column with the rows' activation sums, as the decode GEMV
+//     does, writing the same fp32 partials (one k-split).
+//
+// The LDS exchange stays within a wave (a wave's LDS instructions execute in order), so the
+// waves of a workgroup never synchronise.
+#include "evamx_gemv.hpp"
+#include "evamx_internal.hpp"
+#include "evamx_moe.hpp"
+
+namespace evamx {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int MF_WAVES = 4;                     // waves per workgroup
+constexpr int MF_LDS_WORDS = 8 * 64 * 4;        // per wave: 8 B operands x 64 lanes x 16 bytes
+constexpr int MF_PF = 4;                        // k-slices of weight prefetch (two MFMA k-steps)
+
+__device__ __forceinline__ void wave_lds_fence()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One work item: rows [0, rows) (slots slot_of[0..rows)) of activations src (fp16 [slot][K]
+// with 128-chunk sums) times the decoded weights of tiles 8*cg .. 8*cg+7 of a projection with
+// nk k-slices; writes part[slot * part_stride + 128 * cg + column] for rows < rows.
+template <int K2, int MB>
+__device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, int nt_n, int cg, int nk,
+                                          const GlobalRows& src, const int* __restrict__ slot_of, int rows,
+                                          float* __restrict__ part, size_t part_stride, uint32_t* lds)
+{
+    using R = Rate<K2>;
+    constexpr int K = R::K;
+    constexpr int TW = R::TW;
+    const int lane = threadIdx.x & 63;
+    const int q = lane & 7, ti = lane >> 3;       // decode layout: run q of tile ti
+    const int m16 = lane & 15, g = lane >> 4;     // MFMA layout: row/column m16, k group g
+    nk = __builtin_amdgcn_readfirstlane(nk);
+    const uint32_t slice = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(nt_n * TW));
+    const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW));
+    const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(trellis);
+    uint32_t lane_off, prev_off, sh;
+    lane_offsets<K2>(lane, lane_off, prev_off, sh);
+
+    // A rows of this lane: m16 + 16 mb (rows past the tile read row 0; their results are dropped)
+    const __attribute__((address_space(1))) u32x4_t* arow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int r = m16 + 16 * mb;
+        const int s = slot_of[r < rows ? r : 0];
+        arow[mb] = (const __attribute__((address_space(1))) u32x4_t*)(src.A + (size_t)s * src.stride) + g;
+    }
+
+    f32x4_t acc[MB][8];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    LaneWords<K> ring[MF_PF];
+    const int last = nk - 1;
+#pragma unroll
+    for (int d = 0; d < MF_PF; ++d)
+        load_slice<K>(ring[d], rsrc, cbase + (uint32_t)min(d, last) * slice, lane_off, prev_off);
+
+    u32x4_t a_cur[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) a_cur[mb] = arow[mb][0];
+
+    // LDS slots: B operand nb = tile ti, lane n + 16 g <- (column n = 8c + q, k group g = 2s + kh)
+    uint32_t* wdst = lds + 4 * (64 * ti + q);
+    const uint32_t* rsrc_lds = lds + 4 * lane;
+
+    auto kstep = [&](int kk, LaneWords<K>& w0, LaneWords<K>& w1) {
+        // next step's A operands first: their latency hides behind this step's decode
+        u32x4_t a_nxt[MB];
+        const int kn = kk + 1 < (nk >> 1) ? kk + 1 : kk;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) a_nxt[mb] = arow[mb][4 * kn];
+        wave_lds_fence();
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            LaneWords<K>& w = s == 0 ? w0 : w1;
+            half2_t wp[16];
+            decode_slice<K2>(w, sh, wp);
+            load_slice<K>(w, rsrc, cbase + (uint32_t)min(2 * kk + s + MF_PF, last) * slice, lane_off, prev_off);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh) {
+                    const u32x4_t v = {__builtin_bit_cast(uint32_t, wp[kh + 2 * c]),
+                                       __builtin_bit_cast(uint32_t, wp[kh + 2 * c + 4]),
+                                       __builtin_bit_cast(uint32_t, wp[kh + 2 * c + 8]),
+                                       __builtin_bit_cast(uint32_t, wp[kh + 2 * c + 12])};
+                    *(u32x4_t*)(wdst + 4 * (8 * c + 16 * (2 * s + kh))) = v;
+                }
+        }
+        wave_lds_fence();
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+            const u32x4_t bv = *(const u32x4_t*)(rsrc_lds + 256 * nb);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a_cur[mb]),
+                                                                     __builtin_bit_cast(half8_t, bv), acc[mb][nb], 0, 0, 0);
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) a_cur[mb] = a_nxt[mb];
+    };
+
+    // nk is a multiple of 8 (K a multiple of 128): pairs of ring slots per step, two steps per round
+    for (int kk = 0; kk < (nk >> 1); kk += 2) {
+        kstep(kk, ring[0], ring[1]);
+        kstep(kk + 1, ring[2], ring[3]);
+    }
+
+    // activation sums of the rows over all of K: lane (m16, g) sums chunks g, g + 4, ... of row
+    // m16 + 16 mb; the four k groups are summed across lanes; then each lane fetches the sums of
+    // its output rows 4 g + r.
+    const int nch = nk >> 3;
+    float xs[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int r = m16 + 16 * mb;
+        const int s = slot_of[r < rows ? r : 0];
+        const float* sp = src.sums + (size_t)s * src.sums_stride;
+        float v = 0.0f;
+        for (int c = g; c < nch; c += 4) v += sp[c];
+        v += xor_lane_f<16>(v, lane);
+        v += xor_lane_f<32>(v, lane);
+        xs[mb] = v;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * mb + 4 * g + r;
+            const float xr = __shfl(xs[mb], 4 * g + r, WAVE);
+            if (row < rows) {
+                float* dst = part + (size_t)slot_of[row] * part_stride + 128 * cg + m16;
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) dst[16 * nb] = MUL1_K_INV * acc[mb][nb][r] + MUL1_K_BIAS * xr;
+            }
+        }
+    }
+}
+
+template <int K2>
+__device__ __forceinline__ void mfma_item_rows(const uint32_t* trellis, int nt_n, int cg, int nk, const GlobalRows& src,
+                                               const int* slot_of, int rows, float* part, size_t part_stride,
+                                               uint32_t* lds)
+{
+    const int mb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
+    switch (mb) {
+        case 1: mfma_item<K2, 1>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
+        case 2: mfma_item<K2, 2>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
+        case 3: mfma_item<K2, 3>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
+        default: mfma_item<K2, 4>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
+    }
+}
+
+// Workgroup -> item block with the items of one tile on one XCD: workgroups are dispatched to
+// the 8 XCDs round robin, so consecutive item blocks (a tile's column groups, which share its
+// activation rows) are given to workgroups b, b + 8, b + 16, ... (nb a multiple of 8).
+__device__ __forceinline__ int xcd_item_block(int b, int nb)
+{
+    const int per = nb >> 3;
+    if ((nb & 7) != 0 || per == 0) return b;
+    return (b & 7) * per + (b >> 3);
+}
+
+// which = 0: gate/up (items (tile, proj, cg), cg over I/128) -> part_gu[proj][slot][I];
+// which = 1: down (items (tile, cg), cg over H/128) -> part_d[slot][H].
+__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void moe_mfma_kernel(MoeParams p, int which)
+{
+    __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
+    const int wave = threadIdx.x >> 6;
+    const int n_tiles = __builtin_amdgcn_readfirstlane(p.meta[0]);
+    const int ncg = which == 0 ? p.I / 128 : p.H / 128;
+    const int per_tile = which == 0 ? 2 * ncg : ncg;
+    // the call's items fill the first n_blk workgroups (a multiple of 8, spread over the XCDs)
+    const int n_blk = ((n_tiles * per_tile + MF_WAVES - 1) / MF_WAVES + 7) & ~7;
+    if ((int)blockIdx.x >= n_blk) return;
+    const int blk = xcd_item_block(blockIdx.x, n_blk);
+    const int item = __builtin_amdgcn_readfirstlane(blk * MF_WAVES + wave);
+    const int tile = item / per_tile;
+    if (tile >= n_tiles) return;
+    const int rem = item - tile * per_tile;
+    const int proj = which == 0 ? rem / ncg : 2;
+    const int cg = rem - (which == 0 ? proj * ncg : 0);
+    const int* ch = p.chunks + 8 * tile;
+    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
+    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
+    const int rows = __builtin_amdgcn_readfirstlane(ch[2]);
+    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
+    const int* slot_of = p.order + begin;
+    const int nslot = moe_nslot(p);
+    const int trow = proj == 0 ? EVAMX_TBL_G_TRELLIS : proj == 1 ? EVAMX_TBL_U_TRELLIS : EVAMX_TBL_D_TRELLIS;
+    const uint32_t* trellis = (const uint32_t*)(e < 0 ? (const void*)p.sh_ptr[trow]
+                                                      : (const void*)p.tables[(size_t)trow * p.tbl_stride + e]);
+    GlobalRows src;
+    float* part;
+    size_t part_stride;
+    int nt_n, nk;
+    if (which == 0) {
+        const int nch = p.H / 128;
+        src = GlobalRows{p.xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch, nch};
+        part = p.part_gu + (size_t)proj * nslot * p.I;
+        part_stride = (size_t)p.I;
+        nt_n = p.I / 16;
+        nk = p.H / 16;
+    } else {
+        const int na = p.I / 128;
+        src = GlobalRows{p.act, (size_t)p.I, p.actsum, na};
+        part = p.part_d;
+        part_stride = (size_t)p.H;
+        nt_n = p.H / 16;
+        nk = p.I / 16;
+    }
+    uint32_t* wl = lds[wave];
+    switch (k2) {
+        case 3: mfma_item_rows<3>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 4: mfma_item_rows<4>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 5: mfma_item_rows<5>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 6: mfma_item_rows<6>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 7: mfma_item_rows<7>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 8: mfma_item_rows<8>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 10: mfma_item_rows<10>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        default: {
+            // unsupported rate (flagged by the grouping): zero partials, so no output reads stale data
+            const int lane = threadIdx.x & 63;
+            for (int r = 0; r < rows; ++r) {
+                float* dst = part + (size_t)slot_of[r] * part_stride + 128 * cg;
+                dst[lane] = 0.0f;
+                dst[lane + 64] = 0.0f;
+            }
+        }
+    }
+}
+
+// Launch of one projection stage: enough workgroups for the largest possible tile count
+// (max_tiles, from the workspace layout); workgroups past the call's tiles exit at once.
+int launch_mfma(const MoeParams& p, int which, hipStream_t stream)
+{
+    const int ncg = which == 0 ? p.I / 128 : p.H / 128;
+    const int per_tile = which == 0 ? 2 * ncg : ncg;
+    int blocks = (p.max_chunks * per_tile + MF_WAVES - 1) / MF_WAVES;
+    blocks = (blocks + 7) & ~7;
+    hipLaunchKernelGGL(moe_mfma_kernel, dim3(blocks), dim3(64 * MF_WAVES), 0, stream, p, which);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace evamx

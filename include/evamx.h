@@ -105,9 +105,9 @@ typedef struct evamx_moe_shape {
 typedef struct evamx_moe_args {
     evamx_moe_shape shape;
     int32_t rows;                 /* T, 1..rows_max */
-    const void* x;                /* device [rows][x_stride] fp16 or bf16 */
+    const void* x;                /* device [rows][x_stride] fp16 or bf16, 4-byte aligned */
     int32_t x_dtype;              /* EVAMX_DTYPE_* */
-    int32_t x_stride;             /* elements; >= hidden */
+    int32_t x_stride;             /* elements; even, >= hidden */
     /* routing: logits != NULL routes on device and writes sel/weights/rw_fp16; otherwise
      * sel and weights (fp32) are inputs, or sel and rw_fp16 when weights == NULL */
     const float* logits;          /* device [rows][n_logits] or NULL */
