@@ -600,7 +600,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     const int ncg = p.I / 128;
     const KSplit k = ks_gate_up(p, units);
     const int per_unit = 2 * ncg * k.base;
-    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * 2 * ncg)
+    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * 2 * ncg * ks)
     const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
     if (u >= units) return;
     const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     const int ncg = p.H / 128;
     const KSplit k = ks_down(p, units);
     const int per_unit = ncg * k.base;
-    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * ncg)
+    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * ncg * ks)
     const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
     if (u >= units) return;
     const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
@@ -894,8 +894,10 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
         const int tmax = tmax_for(p.T < EVAMX_CHUNK ? p.T : EVAMX_CHUNK);
         {
-            const int units = EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128);
-            const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
+            // one wave per item: a requested split gives every chunk exactly ks_gu splits, an
+            // automatic one fits the resident grid (moe_ksplit)
+            const long units = (long)EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128) * (p.ks_gu > 0 ? p.ks_gu : 1);
+            const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
             const half_t* xr = p.xr;
             switch (tmax) {
                 case 1: hipLaunchKernelGGL(moe_gate_up_kernel<1>, grid, dim3(256), 0, stream, p, xr); break;
@@ -908,8 +910,8 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         const int waves = nslot * (p.I / 128);
         hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
         mark(3);
-        const int units = EVAMX_MAX_MULT * p.max_chunks * (p.H / 128);
-        const dim3 grid(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4);
+        const long units = (long)EVAMX_MAX_MULT * p.max_chunks * (p.H / 128) * (p.ks_d > 0 ? p.ks_d : 1);
+        const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
         const half_t* act = p.act;
         switch (tmax) {
             case 1: hipLaunchKernelGGL(moe_down_kernel<1>, grid, dim3(256), 0, stream, p, act); break;

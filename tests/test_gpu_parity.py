@@ -122,20 +122,34 @@ def test_moe_layer_small(dev, rows, K):
     assert np.array_equal(runs, coop.reference_table(ridx, rrw, capacity=16))
 
 
+_DSV3_CASES = {}
+
+
+def _dsv3_case(rows):
+    """Seeded DSv3-shape inputs and the oracle output on the touched experts (cached per rows)."""
+    if rows not in _DSV3_CASES:
+        H, I, E, topk, limit, K = 7168, 2048, 256, 8, 10.0, 4
+        rng = np.random.default_rng(42 + rows)
+        x = synth.activations_bf16(rng, rows, H)
+        logits = synth.logits_plain(rng, rows, E) if rows == 1 else synth.logits_skewed(rng, rows, E)
+        ridx, rwt = coop.route(logits, topk)
+        used = sorted(set(int(v) for v in ridx.reshape(-1)))
+        experts = {e: synth.expert(rng, H, I, K, 1 / np.sqrt(H)) for e in used}
+        shared = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
+        ref, _, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+        _DSV3_CASES[rows] = (x, logits, ridx, used, experts, shared, ref)
+    return _DSV3_CASES[rows]
+
+
 @pytest.mark.parametrize("rows", [1, 16])
-def test_moe_layer_dsv3_shape(dev, rows):
+@pytest.mark.parametrize("ks", [(0, 0), (32, 16), (3, 5)])
+def test_moe_layer_dsv3_shape(dev, rows, ks):
     """DeepSeek-V3 shape (H=7168, I=2048, 256 routed + 1 shared, top-8, 4 bpw), oracle on the
-    touched experts only."""
+    touched experts only; automatic k-splits, and requested ones above and below the split that
+    fills the GPU once (every split's partials must be written and summed)."""
     ops = _ops()
     H, I, E, topk, limit, K = 7168, 2048, 256, 8, 10.0, 4
-    rng = np.random.default_rng(42 + rows)
-    x = synth.activations_bf16(rng, rows, H)
-    logits = synth.logits_plain(rng, rows, E) if rows == 1 else synth.logits_skewed(rng, rows, E)
-    ridx, rwt = coop.route(logits, topk)
-    used = sorted(set(int(v) for v in ridx.reshape(-1)))
-    experts = {e: synth.expert(rng, H, I, K, 1 / np.sqrt(H)) for e in used}
-    shared = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
-    ref, _, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+    x, logits, ridx, used, experts, shared, ref = _dsv3_case(rows)
 
     # Device table: touched experts at their indices, a dummy expert everywhere else.
     dummy = synth.expert(np.random.default_rng(0), H, I, K)
@@ -147,7 +161,11 @@ def test_moe_layer_dsv3_shape(dev, rows):
         table[:, e] = host[:, cols.get(e, len(used))]
     table = table.to(dev)
     ds = DeviceExperts([shared], dev)
-    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True,
+                          ksplit_gu=ks[0], ksplit_down=ks[1])
+    # stale partials from an earlier call must not leak into this one
+    ws.buffer.fill_(0x7f)
+    ws.clear_flags()
     sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
     w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
     out = torch.empty(rows, H, dtype=torch.float32, device=dev)
