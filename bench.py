@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE layer decode µs + achieved HBM GB/s (DSv3 shape, 4bpw EXL3, 1/16 tok)"
 PEAK_HBM = 8000.0         # GB/s, MI355X
+PEAK_MFMA_F16 = 2500.0    # TFLOP/s, MI355X dense fp16
 H, I, E, TOPK = 7168, 2048, 256, 8
 STACK_DOWN_SCALE = 0.25   # down-projection svh multiplier of the stacked workload (see DeviceLayers)
 
@@ -341,6 +342,16 @@ def run_layer(torch, args):
     kt = kernel_times(torch, stream, step, n_ev, skip=2 if prefill else 8)
     gu_bytes_launch = sum(layers.gate_up_bytes(i % args.layers, touched[i % n_draws]) for i in range(n_ev)) / n_ev
     roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, args.bits))
+    if prefill:
+        roofline["decode_alu_ceiling"] = decode_ceiling(ops, (2.0, 3.0, 4.0, 5.0))
+        # MFMA utilisation of the gate/up GEMM: 2 * H * I flops per row and projection
+        flops = 2 * H * I * 2 * (T * TOPK + T)
+        roofline["mfma"] = {"kernel": "moe_gate_up", "achieved": round(flops / (kt["moe_gate_up"] * 1e-6) / 1e12, 1),
+                            "peak": PEAK_MFMA_F16, "unit": "TFLOP/s",
+                            "frac": round(flops / (kt["moe_gate_up"] * 1e-6) / 1e12 / PEAK_MFMA_F16, 4),
+                            "flops_per_launch": flops}
+    else:
+        roofline["decode_alu_ceiling"] = decode_ceiling(ops, (args.bits,), roofline["achieved"])
     cfg_idx = 3 if prefill else (1 if T == 1 else 2)
     rates = "per-expert rates {2,3,4,5} (shared 4)" if prefill else f"{args.bits:g} bpw"
     result = {
@@ -432,6 +443,7 @@ def run_stack(torch, args):
     kt = kernel_times(torch, stream, lambda i, events=None: layer(i % L, events), L, skip=0)
     gu_bytes_launch = sum(layers.gate_up_bytes(l, touched[l]) for l in range(L)) / L
     roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, K))
+    roofline["decode_alu_ceiling"] = decode_ceiling(ops, (K,), roofline["achieved"])
     result = {
         "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "us_per_layer": round(ms_step * 1e3 / L, 3),
@@ -458,6 +470,21 @@ def gate_up_roofline(bytes_launch, us, traffic):
     return {"bound": "hbm", "kernel": "moe_gate_up", "achieved": round(achieved, 1), "peak": PEAK_HBM,
             "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": int(bytes_launch), "avg_launch_us": round(us, 3)}
+
+
+def decode_ceiling(ops, bits_list, achieved_gbps=None, weights=None):
+    """Arithmetic bound of the decode GEMV (evamx_bench_decode: the GEMV's per-weight decode and
+    dot-product instructions on register-resident words, no memory traffic), as trellis GB/s at
+    each rate; with one rate, also the fraction of it the dominant kernel reached."""
+    out = {"kernel": "evamx_bench_decode", "unit": "GB/s"}
+    per = {}
+    for b in bits_list:
+        wps = ops.decode_ceiling(b)
+        per[f"{b:g}"] = round(wps * b / 8 / 1e9, 1)
+    out["value"] = per if len(per) > 1 else next(iter(per.values()))
+    if achieved_gbps is not None and len(per) == 1:
+        out["frac"] = round(achieved_gbps / out["value"], 4)
+    return out
 
 
 COPY_BYTES = 1 << 30

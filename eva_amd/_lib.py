@@ -65,6 +65,7 @@ _SIGNATURES = {
     "evamx_moe_forward": (ctypes.c_int, [ctypes.POINTER(MoeArgs), _vp]),
     "evamx_moe_runs_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_moe_flags_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
+    "evamx_bench_decode": (ctypes.c_int, [_f32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
 }
 
 EXPORTS = tuple(_SIGNATURES)

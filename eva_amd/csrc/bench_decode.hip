@@ -1,0 +1,54 @@
+// Decode ALU ceiling: the rate at which gfx950 evaluates the EXL3 trellis decode of the GEMV
+// (window funnels, MUL1 hashes, byte sums into fp16 pairs, one fp16 dot product per pair)
+// when nothing is loaded from memory. Every lane decodes one k-slice's 32 positions per
+// iteration from register-resident words, which it then advances, exactly the per-weight
+// instruction mix of the decode GEMV's inner loop for one row. Bench.py divides the trellis
+// bytes this rate implies into a GEMV's achieved bytes to say how close the GEMV is to the
+// arithmetic bound, as opposed to the HBM bound.
+#include "evamx_gemv.hpp"
+#include "evamx_internal.hpp"
+
+namespace evamx {
+
+template <int K2>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void bench_decode_kernel(float* sink, int iters)
+{
+    using R = Rate<K2>;
+    LaneWords<R::K> w;
+#pragma unroll
+    for (int i = 0; i <= R::K; ++i) w.b[i] = 0x9E3779B9u * (threadIdx.x + 7u * i + 1u) + blockIdx.x;
+    const uint32_t sh = (threadIdx.x & 1) ? 0u : 16u;
+    float a0 = 0.0f, a1 = 0.0f;
+    const half2_t x = {(half_t)0.5f, (half_t)-0.25f};
+    for (int it = 0; it < iters; ++it) {
+        half2_t wp[16];
+        decode_slice<K2>(w, sh, wp);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a0 = dot2(wp[2 * u], x, a0);
+            a1 = dot2(wp[2 * u + 1], x, a1);
+        }
+#pragma unroll
+        for (int i = 0; i <= R::K; ++i) w.b[i] += 0x7F4A7C15u * (i + 1);
+    }
+    // keep the work observable without storing per lane
+    if (a0 + a1 == 1234.5f) sink[threadIdx.x] = a0;
+}
+
+int launch_bench_decode(int k2, int blocks, int iters, float* sink, hipStream_t stream)
+{
+    const dim3 g(blocks), b(256);
+    switch (k2) {
+        case 3: hipLaunchKernelGGL(bench_decode_kernel<3>, g, b, 0, stream, sink, iters); break;
+        case 4: hipLaunchKernelGGL(bench_decode_kernel<4>, g, b, 0, stream, sink, iters); break;
+        case 5: hipLaunchKernelGGL(bench_decode_kernel<5>, g, b, 0, stream, sink, iters); break;
+        case 6: hipLaunchKernelGGL(bench_decode_kernel<6>, g, b, 0, stream, sink, iters); break;
+        case 7: hipLaunchKernelGGL(bench_decode_kernel<7>, g, b, 0, stream, sink, iters); break;
+        case 8: hipLaunchKernelGGL(bench_decode_kernel<8>, g, b, 0, stream, sink, iters); break;
+        case 10: hipLaunchKernelGGL(bench_decode_kernel<10>, g, b, 0, stream, sink, iters); break;
+        default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace evamx

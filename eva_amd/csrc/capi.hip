@@ -374,3 +374,16 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     moe_launch(p, (hipStream_t)stream, a->events);
     return launched("moe_forward");
 }
+
+extern "C" int evamx_bench_decode(float bits, int waves, int iters, float* sink, evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    const int k2 = rate_k2(bits);
+    EVAMX_REQUIRE(sink, "evamx_bench_decode: null sink");
+    EVAMX_REQUIRE(gemv_rate(k2), "evamx_bench_decode: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)bits);
+    EVAMX_REQUIRE(waves >= 4 && waves <= (1 << 22) && waves % 4 == 0, "evamx_bench_decode: waves %d not a multiple of 4 in 4..%d",
+                  waves, 1 << 22);
+    EVAMX_REQUIRE(iters >= 1 && iters <= (1 << 20), "evamx_bench_decode: iters %d outside 1..%d", iters, 1 << 20);
+    launch_bench_decode(k2, waves / 4, iters, sink, (hipStream_t)stream);
+    return launched("bench_decode");
+}

@@ -18,3 +18,9 @@ int launch_linear(const void* x, int rows, int in, int out, const void* trellis,
                   const void* svh, int k2, void* y, void* ws, hipStream_t stream);
 
 }  // namespace evamx
+
+namespace evamx {
+
+int launch_bench_decode(int k2, int blocks, int iters, float* sink, hipStream_t stream);
+
+}  // namespace evamx

@@ -118,9 +118,22 @@ __device__ __forceinline__ uint64_t max_x(uint64_t v, int lane)
     return p > v ? p : v;
 }
 
+// Compare-exchange of two (key, logit) entries into descending key order.
+__device__ __forceinline__ void ce_desc(uint64_t& ka, float& za, uint64_t& kb, float& zb)
+{
+    const bool sw = kb > ka;
+    const uint64_t k = sw ? kb : ka;
+    kb = sw ? ka : kb;
+    ka = k;
+    const float z = sw ? zb : za;
+    zb = sw ? za : zb;
+    za = z;
+}
+
 template <int NPER>
 __device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
 {
+    static_assert(NPER == 4 || NPER == 8, "4 or 8 keys per lane");
     const float* z = p.logits + (size_t)r * p.n_logits;
     float zr[NPER];
     uint64_t key[NPER];
@@ -140,13 +153,23 @@ __device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, h
         }
         key[i] = e < p.n_logits ? pack_key(k, e) : 0ull;
     }
+    // each lane sorts its keys (descending; Batcher networks, checked by the zero-one principle),
+    // so a round's candidate of a lane is its head and the winner's lane just pops it
+    if constexpr (NPER == 4) {
+        ce_desc(key[0], zr[0], key[1], zr[1]); ce_desc(key[2], zr[2], key[3], zr[3]);
+        ce_desc(key[0], zr[0], key[2], zr[2]); ce_desc(key[1], zr[1], key[3], zr[3]);
+        ce_desc(key[1], zr[1], key[2], zr[2]);
+    } else {
+        constexpr int net[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                                    {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+        for (int c = 0; c < 19; ++c) ce_desc(key[net[c][0]], zr[net[c][0]], key[net[c][1]], zr[net[c][1]]);
+    }
     // winners one at a time; lane j keeps winner j's index and logit
     float my_z = 0.0f;
     int my_id = 0;
     for (int j = 0; j < p.topk; ++j) {
-        uint64_t best = 0ull;
-#pragma unroll
-        for (int i = 0; i < NPER; ++i) best = key[i] > best ? key[i] : best;
+        uint64_t best = key[0];
         best = max_x<1>(best, lane);
         best = max_x<2>(best, lane);
         best = max_x<4>(best, lane);
@@ -154,15 +177,15 @@ __device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, h
         best = max_x<16>(best, lane);
         best = max_x<32>(best, lane);
         const int bi = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)best));
-        float mine = 0.0f;
+        const float zb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, zr[0]), bi & 63));
+        if (lane == (bi & 63)) {
 #pragma unroll
-        for (int i = 0; i < NPER; ++i) {
-            if (lane + 64 * i == bi) {
-                key[i] = 0ull;
-                mine = zr[i];
+            for (int i = 0; i + 1 < NPER; ++i) {
+                key[i] = key[i + 1];
+                zr[i] = zr[i + 1];
             }
+            key[NPER - 1] = 0ull;
         }
-        const float zb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), bi & 63));
         if (lane == j) { my_z = zb; my_id = bi; }
     }
     // scores of the winners in parallel, their total in slot order
@@ -225,32 +248,40 @@ __device__ __forceinline__ int wave_incl_scan(int v)
     return v;
 }
 
-// Exclusive scans of four arrays a[k][0..n) in place by one wave, a[k][n] = total (n <= 1024):
-// each lane owns a contiguous block of every array, and the four lane-total scans run together.
-__device__ void wave_excl_scan4(int* a0, int* a1, int* a2, int* a3, int n, int lane)
+// Per-expert offsets by one wave, from the slot counts cnt[0..E): exclusive prefix sums of the
+// counts (off), of the 8-slot runs (run_base), of the chunks of chunk_rows_of(p) slots
+// (chunk_base) and of the GEMV work units (unit_base), each with its total at [E]. Lane l owns
+// experts PER*l .. PER*l + PER-1 in registers; the four lane-total scans run together.
+template <int PER>
+__device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lane)
 {
-    int* const a[4] = {a0, a1, a2, a3};
-    const int per = (n + 63) / 64;
-    const int b0 = lane * per;
-    int sum[4], run[4];
+    const int E = p.n_local;
+    const int cs = 31 - __builtin_clz(chunk_rows_of(p));      // chunk rows are a power of two
+    const int e0 = lane * PER;
+    int v[4][PER], tot[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        sum[k] = 0;
-        for (int i = 0; i < per; ++i)
-            if (b0 + i < n) sum[k] += a[k][b0 + i];
+    for (int i = 0; i < PER; ++i) {
+        const int n = e0 + i < E ? ex.cnt[e0 + i] : 0;
+        v[0][i] = n;
+        v[1][i] = (n + 7) >> 3;
+        v[2][i] = (n + (1 << cs) - 1) >> cs;
+        v[3][i] = expert_units(n);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) tot[k] += v[k][i];
     }
+    int run[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) run[k] = wave_incl_scan(sum[k]);
+    for (int k = 0; k < 4; ++k) run[k] = wave_incl_scan(tot[k]);
+    int* const dst[4] = {ex.off, ex.run_base, ex.chunk_base, ex.unit_base};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        int r = run[k] - sum[k];
-        for (int i = 0; i < per; ++i)
-            if (b0 + i < n) {
-                const int v = a[k][b0 + i];
-                a[k][b0 + i] = r;
-                r += v;
-            }
-        if (lane == 63) a[k][n] = run[k];
+        int r = run[k] - tot[k];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            if (e0 + i < E) dst[k][e0 + i] = r;
+            r += v[k][i];
+        }
+        if (lane == 63) dst[k][E] = run[k];
     }
 }
 
@@ -287,13 +318,8 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
     }
     __syncthreads();
     if (wave == 0) {
-        for (int e = lane; e < E; e += 64) {
-            ex.off[e] = ex.cnt[e];
-            ex.run_base[e] = (ex.cnt[e] + 7) / 8;
-            ex.chunk_base[e] = (ex.cnt[e] + chunk_rows_of(p) - 1) / chunk_rows_of(p);
-            ex.unit_base[e] = expert_units(ex.cnt[e]);
-        }
-        wave_excl_scan4(ex.off, ex.run_base, ex.chunk_base, ex.unit_base, E, lane);
+        if (E <= 256) expert_offsets<4>(p, ex, lane);
+        else expert_offsets<EVAMX_MAX_EXPERTS / 64>(p, ex, lane);
         // Stable scatter by (expert, slot): blocks of 64 slots in order; lanes holding the same
         // expert find each other with one ballot per expert-index bit.
         for (int s0 = 0; s0 < slots; s0 += 64) {

@@ -217,3 +217,21 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     check(lib().evamx_moe_forward(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward")
     del keep
     return out
+
+
+def decode_ceiling(bits: float, device=None, waves: int | None = None, iters: int = 4000) -> float:
+    """Decoded weights per second of the register-only decode benchmark (evamx_bench_decode):
+    the arithmetic bound of the decode GEMV at ``bits``, timed with events on the current stream."""
+    dev = torch.device("cuda", 0) if device is None else torch.device(device)
+    if waves is None:
+        waves = torch.cuda.get_device_properties(dev).multi_processor_count * 16
+    sink = torch.zeros(256, dtype=torch.float32, device=dev)
+    stream = stream_handle(dev)
+    check(lib().evamx_bench_decode(float(bits), waves, 16, ptr(sink), stream), "evamx_bench_decode")   # warm-up
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    check(lib().evamx_bench_decode(float(bits), waves, iters, ptr(sink), stream), "evamx_bench_decode")
+    e1.record()
+    e1.synchronize()
+    return waves * 64.0 * 32.0 * iters / (e0.elapsed_time(e1) * 1e-3)

@@ -156,6 +156,16 @@ int evamx_moe_forward(const evamx_moe_args* args, evamx_stream_t stream);
 int32_t* evamx_moe_runs_ptr(const evamx_moe_shape* shape, void* workspace);
 int32_t* evamx_moe_flags_ptr(const evamx_moe_shape* shape, void* workspace);
 
+/* ---- measurement --------------------------------------------------------------------------- */
+
+/* No counterpart in the reference: a benchmark kernel for the arithmetic bound of the decode
+ * GEMV. `waves` waves each decode `iters` k-slices (32 weights per lane) of register-resident
+ * trellis words at rate `bits` with one fp16 dot product per weight pair, the GEMV's
+ * per-weight instruction mix without its memory traffic; time it with events on `stream`.
+ * Weights decoded = waves * 64 * 32 * iters. sink: device float[256] (written only to keep the
+ * work observable). */
+int evamx_bench_decode(float bits, int waves, int iters, float* sink, evamx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -153,3 +153,12 @@ def test_graph_replays(dev):
         ref, ridx, _, _ = coop.moe_layer(x, z, ex, sh, k, 10.0)
         assert np.array_equal(idx_graph.cpu().numpy(), ridx)
         assert rel_err_rows(y_graph.cpu().numpy(), ref) < TOL
+
+
+def test_decode_ceiling_benchmark(dev):
+    """The register-only decode benchmark runs at every GEMV rate and reports a plausible rate
+    (between 1e12 and 1e14 weights/s on one MI355X)."""
+    from eva_amd import ops
+    for bits in (1.5, 2.0, 2.5, 3.0, 3.5, 4.0, 5.0):
+        wps = ops.decode_ceiling(bits, dev, iters=200)
+        assert 1e12 < wps < 1e14, (bits, wps)
