@@ -11,6 +11,7 @@ constexpr int EVAMX_MAX_EXPERTS = 512;     // pointer-table entries per layer (r
 constexpr int EVAMX_MAX_TOPK = 32;         // reference bound: top_k <= 32 (exl3_moe_coop_kernel.cuh:46)
 constexpr int EVAMX_CHUNK = 8;             // slots of one expert per GEMV work item
 constexpr int EVAMX_TILE_ROWS = 64;        // slots of one expert per MFMA work item
+constexpr int EVAMX_MFMA_MIN_ROWS = 8;     // calls with at least this many rows take the MFMA path
 
 // Pointer-table rows, in the reference's order (ds41/cache.py:1877-1886).
 enum {
@@ -23,7 +24,8 @@ enum { PREP_GROUP = 1, PREP_MOE = 2 };
 
 struct MoeParams {
     int mode;
-    int mfma;                  // 1: expert GEMMs on the MFMA path (tiles of EVAMX_TILE_ROWS, one k-split)
+    int mfma;                  // 1: expert GEMMs on the MFMA path (chunks of chunk_rows as tiles, each
+                               // one work unit of weight 1)
     int chunk_rows;            // rows per GEMV chunk / MFMA tile (0: EVAMX_CHUNK)
     int T, H, I, topk, n_local, n_logits;
     // input rows
@@ -117,13 +119,11 @@ __device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
 
 __device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
 {
-    if (p.mfma) return KSplit{1, 1};
     return moe_ksplit(p.ks_gu, units * 2 * (p.I / 128), p.gemv_waves, p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
 }
 
 __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
 {
-    if (p.mfma) return KSplit{1, 1};
     return moe_ksplit(p.ks_d, units * (p.H / 128), p.gemv_waves, p.ks_d_max, p.cap_rows_d, moe_nslot(p));
 }
 

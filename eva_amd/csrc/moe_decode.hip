@@ -265,7 +265,7 @@ __device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lane)
         v[0][i] = n;
         v[1][i] = (n + 7) >> 3;
         v[2][i] = (n + (1 << cs) - 1) >> cs;
-        v[3][i] = expert_units(n);
+        v[3][i] = p.mfma ? v[2][i] : expert_units(n);          // MFMA tiles are one unit each
 #pragma unroll
         for (int k = 0; k < 4; ++k) tot[k] += v[k][i];
     }
@@ -367,7 +367,7 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
         for (int j = 0; j * CR < n; ++j) {
             const int ci = ex.chunk_base[e] + j;
             const int rows = min(CR, n - j * CR);
-            const int m = chunk_mult(rows);
+            const int m = p.mfma ? 1 : chunk_mult(rows);
             int* c = p.chunks + 8 * ci;
             c[0] = e;
             c[1] = ex.off[e] + j * CR;
@@ -378,10 +378,9 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             c[5] = m;
             c[6] = 0;
             c[7] = 0;
-            if (!p.mfma) {
-                for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
+            for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
+            if (!p.mfma)                 // MFMA tiles weigh 1: filled in parallel below
                 for (int i = 0; i < rows; ++i) p.slot_mult[order[c[1] + i]] = m;
-            }
             u += m;
         }
     }
@@ -391,8 +390,8 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
         const int slots = p.T * p.topk;
         for (int j = t; j < nsc; j += nt) {
             const int rows = min(CR, p.T - j * CR);
-            const int m = chunk_mult(rows);
-            const int u = ex.unit_base[E] + j * chunk_mult(CR);     // earlier chunks are full
+            const int m = p.mfma ? 1 : chunk_mult(rows);
+            const int u = ex.unit_base[E] + j * (p.mfma ? 1 : chunk_mult(CR));     // earlier chunks are full
             int* c = p.chunks + 8 * (base + j);
             c[0] = -1;
             c[1] = n_active + j * CR;
@@ -402,12 +401,13 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             c[5] = m;
             c[6] = 0;
             c[7] = 0;
-            if (!p.mfma) {
-                for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
+            for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
+            if (!p.mfma)
                 for (int i = 0; i < rows; ++i) p.slot_mult[slots + j * CR + i] = m;
-            }
         }
     }
+    if (p.mfma)
+        for (int s = t; s < moe_nslot(p); s += nt) p.slot_mult[s] = 1;
 }
 
 __device__ __forceinline__ int total_chunks(const MoeParams& p, const ExpertLds& ex)
@@ -417,7 +417,8 @@ __device__ __forceinline__ int total_chunks(const MoeParams& p, const ExpertLds&
 
 __device__ __forceinline__ int total_units(const MoeParams& p, const ExpertLds& ex)
 {
-    return ex.unit_base[p.n_local] + (p.has_shared ? expert_units(p.T) : 0);
+    const int CR = chunk_rows_of(p);
+    return ex.unit_base[p.n_local] + (p.has_shared ? (p.mfma ? (p.T + CR - 1) / CR : expert_units(p.T)) : 0);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -676,9 +677,8 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const half_t* u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
     const half_t* d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
     const float L = p.limit;
-    // the MFMA path writes one split and no chunk weights
-    const int Sg = p.mfma ? 1 : ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
-                                            __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
+    const int Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
+                               __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
     const int nslot = moe_nslot(p);
     float g[2], u[2];
 #pragma unroll
@@ -833,7 +833,7 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
         const half_t* svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
                                    : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
         float v[2];
-        sum_partials(p, sk, cg, lane, p.mfma ? 1 : ks_of_chunk(ks_down(p, units), mult), v);
+        sum_partials(p, sk, cg, lane, ks_of_chunk(ks_down(p, units), mult), v);
         const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
         if (shared) {
             v[0] = h2f(f2h(v[0]));                     // EXL3 linear C in fp16
@@ -895,8 +895,8 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     const int nch = p.H / 128;
     const int nslot = p.T * p.topk + (p.has_shared ? p.T : 0);
     const bool small = moe_small_path(p.T, p.topk);
-    p.mfma = small ? 0 : 1;
-    p.chunk_rows = small ? EVAMX_CHUNK : EVAMX_TILE_ROWS;
+    p.mfma = p.T >= EVAMX_MFMA_MIN_ROWS ? 1 : 0;
+    p.chunk_rows = p.mfma ? EVAMX_TILE_ROWS : EVAMX_CHUNK;
     mark(0);
     if (small) {
         int blocks = (nslot * nch * 2 + 3) / 4;

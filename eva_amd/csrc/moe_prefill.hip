@@ -40,10 +40,11 @@ __device__ __forceinline__ void wave_lds_fence()
 }
 
 // One work item: rows [0, rows) (slots slot_of[0..rows)) of activations src (fp16 [slot][K]
-// with 128-chunk sums) times the decoded weights of tiles 8*cg .. 8*cg+7 of a projection with
-// nk k-slices; writes part[slot * part_stride + 128 * cg + column] for rows < rows.
+// with 128-chunk sums) times the decoded weights of tiles 8*cg .. 8*cg+7 of a projection over
+// the k-slices [kt0, kt1) (whole 128-chunks); writes part[slot * part_stride + 128 * cg +
+// column] for rows < rows.
 template <int K2, int MB>
-__device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, int nt_n, int cg, int nk,
+__device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
                                           const GlobalRows& src, const int* __restrict__ slot_of, int rows,
                                           float* __restrict__ part, size_t part_stride, uint32_t* lds)
 {
@@ -53,9 +54,10 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
     const int lane = threadIdx.x & 63;
     const int q = lane & 7, ti = lane >> 3;       // decode layout: run q of tile ti
     const int m16 = lane & 15, g = lane >> 4;     // MFMA layout: row/column m16, k group g
-    nk = __builtin_amdgcn_readfirstlane(nk);
+    kt0 = __builtin_amdgcn_readfirstlane(kt0);
+    const int nk = __builtin_amdgcn_readfirstlane(kt1) - kt0;
     const uint32_t slice = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(nt_n * TW));
-    const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW));
+    const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW) + (uint32_t)kt0 * 4u * (uint32_t)(nt_n * TW));
     const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(trellis);
     uint32_t lane_off, prev_off, sh;
     lane_offsets<K2>(lane, lane_off, prev_off, sh);
@@ -66,7 +68,7 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
     for (int mb = 0; mb < MB; ++mb) {
         const int r = m16 + 16 * mb;
         const int s = slot_of[r < rows ? r : 0];
-        arow[mb] = (const __attribute__((address_space(1))) u32x4_t*)(src.A + (size_t)s * src.stride) + g;
+        arow[mb] = (const __attribute__((address_space(1))) u32x4_t*)(src.A + (size_t)s * src.stride + 16 * kt0) + g;
     }
 
     f32x4_t acc[MB][8];
@@ -126,16 +128,16 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
         for (int mb = 0; mb < MB; ++mb) a_cur[mb] = a_nxt[mb];
     };
 
-    // nk is a multiple of 8 (K a multiple of 128): pairs of ring slots per step, two steps per round
+    // nk is a multiple of 8 (whole 128-chunks): pairs of ring slots per step, two steps per round
     for (int kk = 0; kk < (nk >> 1); kk += 2) {
         kstep(kk, ring[0], ring[1]);
         kstep(kk + 1, ring[2], ring[3]);
     }
 
-    // activation sums of the rows over all of K: lane (m16, g) sums chunks g, g + 4, ... of row
-    // m16 + 16 mb; the four k groups are summed across lanes; then each lane fetches the sums of
-    // its output rows 4 g + r.
-    const int nch = nk >> 3;
+    // activation sums of the rows over the item's chunks: lane (m16, g) sums chunks c0 + g,
+    // c0 + g + 4, ... of row m16 + 16 mb; the four k groups are summed across lanes; then each
+    // lane fetches the sums of its output rows 4 g + r.
+    const int c0 = kt0 >> 3, c1 = c0 + (nk >> 3);
     float xs[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -143,7 +145,7 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
         const int s = slot_of[r < rows ? r : 0];
         const float* sp = src.sums + (size_t)s * src.sums_stride;
         float v = 0.0f;
-        for (int c = g; c < nch; c += 4) v += sp[c];
+        for (int c = c0 + g; c < c1; c += 4) v += sp[c];
         v += xor_lane_f<16>(v, lane);
         v += xor_lane_f<32>(v, lane);
         xs[mb] = v;
@@ -163,17 +165,21 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
     }
 }
 
-template <int K2>
-__device__ __forceinline__ void mfma_item_rows(const uint32_t* trellis, int nt_n, int cg, int nk, const GlobalRows& src,
-                                               const int* slot_of, int rows, float* part, size_t part_stride,
-                                               uint32_t* lds)
+template <int K2, int MBMAX>
+__device__ __forceinline__ void mfma_item_rows(const uint32_t* trellis, int nt_n, int cg, int kt0, int kt1,
+                                               const GlobalRows& src, const int* slot_of, int rows, float* part,
+                                               size_t part_stride, uint32_t* lds)
 {
-    const int mb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
-    switch (mb) {
-        case 1: mfma_item<K2, 1>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
-        case 2: mfma_item<K2, 2>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
-        case 3: mfma_item<K2, 3>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
-        default: mfma_item<K2, 4>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, lds); break;
+    if constexpr (MBMAX == 1) {
+        mfma_item<K2, 1>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds);
+    } else {
+        const int mb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
+        switch (mb) {
+            case 1: mfma_item<K2, 1>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 2: mfma_item<K2, 2>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 3: mfma_item<K2, 3>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            default: mfma_item<K2, 4>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+        }
     }
 }
 
@@ -187,15 +193,22 @@ __device__ __forceinline__ int xcd_item_block(int b, int nb)
     return (b & 7) * per + (b >> 3);
 }
 
-// which = 0: gate/up (items (tile, proj, cg), cg over I/128) -> part_gu[proj][slot][I];
-// which = 1: down (items (tile, cg), cg over H/128) -> part_d[slot][H].
-__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void moe_mfma_kernel(MoeParams p, int which)
+// which = 0: gate/up, items (tile, proj, cg, ks) with cg over I/128 -> part_gu[ks][proj][slot][I];
+// which = 1: down, items (tile, cg, ks) with cg over H/128 -> part_d[ks][slot][H].
+// Every tile is one work unit of weight 1; the k-split is the decode GEMV's (moe_ksplit: as many
+// splits as fill the resident grid once, or the requested count), so the activation and combine
+// kernels sum the same partials. MBMAX bounds the tile rows in 16-row blocks (1: at most 16 rows,
+// i.e. calls of at most 16 tokens, with a quarter of the accumulators).
+template <int MBMAX>
+__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(MBMAX == 1 ? 3 : 2))) void moe_mfma_kernel(MoeParams p, int which)
 {
     __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
     const int wave = threadIdx.x >> 6;
     const int n_tiles = __builtin_amdgcn_readfirstlane(p.meta[0]);
     const int ncg = which == 0 ? p.I / 128 : p.H / 128;
-    const int per_tile = which == 0 ? 2 * ncg : ncg;
+    const KSplit k = which == 0 ? ks_gate_up(p, n_tiles) : ks_down(p, n_tiles);
+    const int S = ks_of_chunk(k, 1);
+    const int per_tile = (which == 0 ? 2 * ncg : ncg) * S;
     // the call's items fill the first n_blk workgroups (a multiple of 8, spread over the XCDs)
     const int n_blk = ((n_tiles * per_tile + MF_WAVES - 1) / MF_WAVES + 7) & ~7;
     if ((int)blockIdx.x >= n_blk) return;
@@ -204,8 +217,10 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     const int tile = item / per_tile;
     if (tile >= n_tiles) return;
     const int rem = item - tile * per_tile;
-    const int proj = which == 0 ? rem / ncg : 2;
-    const int cg = rem - (which == 0 ? proj * ncg : 0);
+    const int ks = rem % S;
+    const int pc = rem / S;
+    const int proj = which == 0 ? pc / ncg : 2;
+    const int cg = pc - (which == 0 ? proj * ncg : 0);
     const int* ch = p.chunks + 8 * tile;
     const int e = __builtin_amdgcn_readfirstlane(ch[0]);
     const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
@@ -219,31 +234,30 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     GlobalRows src;
     float* part;
     size_t part_stride;
-    int nt_n, nk;
+    int nt_n, nch;
     if (which == 0) {
-        const int nch = p.H / 128;
+        nch = p.H / 128;
         src = GlobalRows{p.xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch, nch};
-        part = p.part_gu + (size_t)proj * nslot * p.I;
+        part = p.part_gu + ((size_t)ks * 2 + proj) * nslot * p.I;
         part_stride = (size_t)p.I;
         nt_n = p.I / 16;
-        nk = p.H / 16;
     } else {
-        const int na = p.I / 128;
-        src = GlobalRows{p.act, (size_t)p.I, p.actsum, na};
-        part = p.part_d;
+        nch = p.I / 128;
+        src = GlobalRows{p.act, (size_t)p.I, p.actsum, nch};
+        part = p.part_d + (size_t)ks * nslot * p.H;
         part_stride = (size_t)p.H;
         nt_n = p.H / 16;
-        nk = p.I / 16;
     }
+    const int kt0 = 8 * (nch * ks / S), kt1 = 8 * (nch * (ks + 1) / S);
     uint32_t* wl = lds[wave];
     switch (k2) {
-        case 3: mfma_item_rows<3>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
-        case 4: mfma_item_rows<4>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
-        case 5: mfma_item_rows<5>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
-        case 6: mfma_item_rows<6>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
-        case 7: mfma_item_rows<7>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
-        case 8: mfma_item_rows<8>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
-        case 10: mfma_item_rows<10>(trellis, nt_n, cg, nk, src, slot_of, rows, part, part_stride, wl); break;
+        case 3: mfma_item_rows<3, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
+        case 4: mfma_item_rows<4, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
+        case 5: mfma_item_rows<5, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
+        case 6: mfma_item_rows<6, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
+        case 7: mfma_item_rows<7, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
+        case 8: mfma_item_rows<8, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
+        case 10: mfma_item_rows<10, MBMAX>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, wl); break;
         default: {
             // unsupported rate (flagged by the grouping): zero partials, so no output reads stale data
             const int lane = threadIdx.x & 63;
@@ -256,15 +270,24 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     }
 }
 
-// Launch of one projection stage: enough workgroups for the largest possible tile count
-// (max_tiles, from the workspace layout); workgroups past the call's tiles exit at once.
+// Launch of one projection stage: enough workgroups for the largest possible item count (the
+// workspace's tile bound times the largest split); workgroups past the call's items exit at once.
 int launch_mfma(const MoeParams& p, int which, hipStream_t stream)
 {
     const int ncg = which == 0 ? p.I / 128 : p.H / 128;
-    const int per_tile = which == 0 ? 2 * ncg : ncg;
-    int blocks = (p.max_chunks * per_tile + MF_WAVES - 1) / MF_WAVES;
-    blocks = (blocks + 7) & ~7;
-    hipLaunchKernelGGL(moe_mfma_kernel, dim3(blocks), dim3(64 * MF_WAVES), 0, stream, p, which);
+    const int kreq = which == 0 ? p.ks_gu : p.ks_d;
+    const int kmax = which == 0 ? p.ks_gu_max : p.ks_d_max;
+    const long per_tile = (long)(which == 0 ? 2 * ncg : ncg);
+    const long auto_items = (long)p.gemv_waves + per_tile;   // an automatic split fills one resident round
+    const long items = kreq > 0 ? (long)p.max_chunks * per_tile * kreq
+                                : (p.max_chunks * per_tile > auto_items ? (long)p.max_chunks * per_tile : auto_items);
+    (void)kmax;
+    long blocks = (items + MF_WAVES - 1) / MF_WAVES;
+    blocks = (blocks + 7) & ~7L;
+    if (p.T <= 16)
+        hipLaunchKernelGGL(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), 0, stream, p, which);
+    else
+        hipLaunchKernelGGL(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), 0, stream, p, which);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
