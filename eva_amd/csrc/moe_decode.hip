@@ -352,6 +352,92 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
     __syncthreads();
 }
 
+// The same grouping for many slots by a workgroup of GROUP_WAVES waves: wave w owns the
+// contiguous slot range [w*per, (w+1)*per); per-wave expert histograms give every wave the
+// offsets of its first slot of each expert, so all waves scatter at once and the order stays
+// stable by (expert, slot). local/order live in global memory.
+constexpr int GROUP_WAVES = 16;
+
+struct GroupLds {
+    int hist[GROUP_WAVES][EVAMX_MAX_EXPERTS];
+};
+
+template <typename SelT>
+__device__ void group_slots_par(const MoeParams& p, const SelT* sel, const half_t* rw, int slots, int* local,
+                                int* order, ExpertLds& ex, GroupLds& gl, bool publish)
+{
+    const int t = threadIdx.x, nt = blockDim.x, lane = t & 63, wave = t >> 6;
+    const int E = p.n_local;
+    for (int i = t; i < GROUP_WAVES * EVAMX_MAX_EXPERTS; i += nt) (&gl.hist[0][0])[i] = 0;
+    __syncthreads();
+    const int per = (slots + GROUP_WAVES - 1) / GROUP_WAVES;
+    const int s0 = wave * per, s1 = min(slots, s0 + per);
+    for (int s = s0 + lane; s < s1; s += 64) {
+        const int64_t e = (int64_t)sel[s];
+        const float w = h2f(rw[s]);
+        int lo = -1;
+        if (w != 0.0f) {
+            int64_t le = e;
+            bool ok = true;
+            if (p.min_expert >= 0) {
+                ok = e >= p.min_expert && e < p.max_expert;
+                le = e - p.min_expert;
+            }
+            if (ok) {
+                if (le < 0 || le >= E) {
+                    if (publish) atomicOr(p.err, EVAMX_ERR_EXPERT_RANGE);
+                } else lo = (int)le;
+            }
+        }
+        local[s] = lo;
+        if (lo >= 0) atomicAdd(&gl.hist[wave][lo], 1);
+    }
+    __syncthreads();
+    // per-wave exclusive offsets within each expert (in place) and the expert totals
+    for (int e = t; e < E; e += nt) {
+        int run = 0;
+#pragma unroll
+        for (int w = 0; w < GROUP_WAVES; ++w) {
+            const int c = gl.hist[w][e];
+            gl.hist[w][e] = run;
+            run += c;
+        }
+        ex.cnt[e] = run;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        if (E <= 256) expert_offsets<4>(p, ex, lane);
+        else expert_offsets<EVAMX_MAX_EXPERTS / 64>(p, ex, lane);
+    }
+    __syncthreads();
+    for (int b = s0; b < s1; b += 64) {
+        const int s = b + lane;
+        const int e = s < s1 ? local[s] : -1;      // this lane's own store above
+        const bool act = e >= 0;
+        uint64_t m = __ballot(act);
+#pragma unroll
+        for (int bit = 0; bit < 10; ++bit) {
+            const bool v = act && ((e >> bit) & 1);
+            const uint64_t bb = __ballot(v);
+            m &= v ? bb : ~bb;
+        }
+        const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        if (act) {
+            const int rank = gl.hist[wave][e] + __popcll(m & lt);
+            const int pos = ex.off[e] + rank;
+            if (order) order[pos] = s;
+            if (publish && p.runs) {
+                p.runs[2 + p.slots_max + 1 + pos] = s;
+                if ((rank & 7) == 0) p.runs[2 + ex.run_base[e] + rank / 8] = pos;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (act && (m & lt) == 0) gl.hist[wave][e] += __popcll(m);
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+}
+
 // Chunks of <= chunk_rows_of(p) slots per expert, then the shared expert's rows; for the decode
 // GEMV also their work units (unit -> chunk map) and each slot's chunk weight. `order` is the
 // grouped slot order.
@@ -569,9 +655,10 @@ __global__ __launch_bounds__(256) void moe_route_kernel(MoeParams p)
     if (r < p.T) route_token(p, r, lane, nullptr, nullptr, true);
 }
 
-__global__ __launch_bounds__(1024) void moe_group_kernel(MoeParams p)
+__global__ __launch_bounds__(64 * GROUP_WAVES) void moe_group_kernel(MoeParams p)
 {
     __shared__ ExpertLds ex;
+    __shared__ GroupLds gl;
     const int t = threadIdx.x;
     const int slots = p.T * p.topk;
     if (!p.logits && p.weights)
@@ -581,7 +668,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(MoeParams p)
         for (int i = t; i < table_len; i += 1024) p.runs[i] = 0;
     }
     __syncthreads();
-    group_slots(p, p.sel, p.rw16, slots, p.local, p.order, ex, true);
+    group_slots_par(p, p.sel, p.rw16, slots, p.local, p.order, ex, gl, true);
     const int n_active = ex.off[p.n_local];
     if (t == 0 && p.runs) {
         p.runs[0] = ex.run_base[p.n_local];
@@ -661,14 +748,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
 // 784-805 for routed slots (act_gate with the clamp after SiLU) or the shared expert's EXL3
 // linear outputs + swiglu (model.py:450-452, kernels.py:213-217), and the down projection's
 // input rotation; writes act (fp16) and the chunk's sum.
+template <int CPW>
 __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
 {
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int na = p.I / 128;
+    const int ng = na / CPW;                 // chunk groups per row (CPW divides na)
     const int n_rows = p.meta[1] + (p.has_shared ? p.T : 0);
-    if (wid >= n_rows * na) return;
-    const int o = wid / na, a = wid % na;
+    if (wid >= n_rows * ng) return;
+    const int o = wid / ng, a0 = (wid % ng) * CPW;
     const int slots = p.T * p.topk;
     const int s = __builtin_amdgcn_readfirstlane(p.order[o]);
     const int e = s < slots ? __builtin_amdgcn_readfirstlane(p.local[s]) : -1;
@@ -680,68 +769,96 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const int Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
                                __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
     const int nslot = moe_nslot(p);
-    float g[2], u[2];
+    // all chunks' partial sums and scales first, so their loads are in flight together
+    float g[CPW][2], u[CPW][2], gs[CPW][2], us[CPW][2], ds[CPW][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int col = a * 128 + lane_col(lane, h);
-        const float* pg = p.part_gu + (size_t)s * p.I + col;
-        const size_t pstride = (size_t)2 * nslot * p.I;              // next k-split
-        const size_t ustride = (size_t)nslot * p.I;                  // gate -> up
-        float sg = 0.0f, su = 0.0f;
-        int q = 0;
-        for (; q + 4 <= Sg; q += 4) {
-            float tg[4], tu[4];
+    for (int c = 0; c < CPW; ++c) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                tg[i] = pg[(q + i) * pstride];
-                tu[i] = pg[(q + i) * pstride + ustride];
+        for (int h = 0; h < 2; ++h) {
+            const int col = (a0 + c) * 128 + lane_col(lane, h);
+            const float* pg = p.part_gu + (size_t)s * p.I + col;
+            const size_t pstride = (size_t)2 * nslot * p.I;              // next k-split
+            const size_t ustride = (size_t)nslot * p.I;                  // gate -> up
+            float sg = 0.0f, su = 0.0f;
+            int q = 0;
+            for (; q + 4 <= Sg; q += 4) {
+                float tg[4], tu[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    tg[i] = pg[(q + i) * pstride];
+                    tu[i] = pg[(q + i) * pstride + ustride];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) { sg += tg[i]; su += tu[i]; }
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { sg += tg[i]; su += tu[i]; }
-        }
-        for (; q < Sg; ++q) {
-            sg += pg[q * pstride];
-            su += pg[q * pstride + ustride];
-        }
-        g[h] = h2f(f2h(sg));     // GEMV output stored as fp16 (gu_f32 = false)
-        u[h] = h2f(f2h(su));
-    }
-    had128_lane(g[0], g[1], lane);
-    had128_lane(u[0], u[1], lane);
-    float av[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int col = a * 128 + lane_col(lane, h);
-        const float gs = h2f(g_svh[col]), us = h2f(u_svh[col]), ds = h2f(d_suh[col]);
-        if (shared) {
-            // EXL3 linear outputs: fp16 after the rotation, fp16 product with svh; swiglu clamps
-            // the gate BEFORE SiLU; mid to fp16; fp16 product with the down projection's suh
-            float gv = h2f(f2h(h2f(f2h(g[h])) * gs));
-            float uv = h2f(f2h(h2f(f2h(u[h])) * us));
-            if (L > 0.0f) {
-                uv = fminf(fmaxf(uv, -L), L);
-                gv = fminf(gv, L);
+            for (; q < Sg; ++q) {
+                sg += pg[q * pstride];
+                su += pg[q * pstride + ustride];
             }
-            const float mid = h2f(f2h(silu_f(gv) * uv));
-            av[h] = h2f(f2h(mid * ds));
-        } else {
-            const float gv = g[h] * gs;
-            float uv = u[h] * us;
-            float x = silu_f(gv);
-            if (L != 0.0f) {
-                uv = fminf(fmaxf(uv, -L), L);
-                x = fminf(x, L);
-            }
-            av[h] = x * uv * ds;
+            g[c][h] = sg;
+            u[c][h] = su;
+            gs[c][h] = h2f(g_svh[col]);
+            us[c][h] = h2f(u_svh[col]);
+            ds[c][h] = h2f(d_suh[col]);
         }
     }
-    had128_lane(av[0], av[1], lane);
-    half_t* dst = p.act + (size_t)s * p.I + a * 128;
-    const half_t r0 = f2h(av[0]), r1 = f2h(av[1]);
-    dst[lane_col(lane, 0)] = r0;
-    dst[lane_col(lane, 1)] = r1;
-    const float sum = wave_sum(h2f(r0) + h2f(r1));
-    if (lane == 0) p.actsum[(size_t)s * na + a] = sum;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        float gg[2], uu[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            gg[h] = h2f(f2h(g[c][h]));     // GEMV output stored as fp16 (gu_f32 = false)
+            uu[h] = h2f(f2h(u[c][h]));
+        }
+        had128_lane(gg[0], gg[1], lane);
+        had128_lane(uu[0], uu[1], lane);
+        float av[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (shared) {
+                // EXL3 linear outputs: fp16 after the rotation, fp16 product with svh; swiglu
+                // clamps the gate BEFORE SiLU; mid to fp16; fp16 product with the down suh
+                float gv = h2f(f2h(h2f(f2h(gg[h])) * gs[c][h]));
+                float uv = h2f(f2h(h2f(f2h(uu[h])) * us[c][h]));
+                if (L > 0.0f) {
+                    uv = fminf(fmaxf(uv, -L), L);
+                    gv = fminf(gv, L);
+                }
+                const float mid = h2f(f2h(silu_f(gv) * uv));
+                av[h] = h2f(f2h(mid * ds[c][h]));
+            } else {
+                const float gv = gg[h] * gs[c][h];
+                float uv = uu[h] * us[c][h];
+                float x = silu_f(gv);
+                if (L != 0.0f) {
+                    uv = fminf(fmaxf(uv, -L), L);
+                    x = fminf(x, L);
+                }
+                av[h] = x * uv * ds[c][h];
+            }
+        }
+        had128_lane(av[0], av[1], lane);
+        half_t* dst = p.act + (size_t)s * p.I + (a0 + c) * 128;
+        const half_t r0 = f2h(av[0]), r1 = f2h(av[1]);
+        dst[lane_col(lane, 0)] = r0;
+        dst[lane_col(lane, 1)] = r1;
+        const float sum = wave_sum(h2f(r0) + h2f(r1));
+        if (lane == 0) p.actsum[(size_t)s * na + a0 + c] = sum;
+    }
+}
+
+// Activation launch: one wave per (row, chunk) for small batches (latency), per (row, 4 chunks)
+// for large ones (the row's slot, expert and pointers resolved once).
+static void launch_act(const MoeParams& p, int nslot, hipStream_t stream)
+{
+    const int na = p.I / 128;
+    if (p.T > EVAMX_SMALL_ROWS && na % 4 == 0) {
+        const int waves = nslot * (na / 4);
+        hipLaunchKernelGGL(moe_act_kernel<4>, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+    } else {
+        const int waves = nslot * na;
+        hipLaunchKernelGGL(moe_act_kernel<1>, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+    }
 }
 
 // Down GEMV: one wave per work item (chunk, 128 columns, k-split) -> part_d[ks][slot][H].
@@ -800,9 +917,42 @@ __device__ __forceinline__ void sum_partials(const MoeParams& p, int s, int cg, 
     }
 }
 
-// Per-token reduction over slots in slot order (+ shared expert). One workgroup per (token,
-// 128 columns) with one wave per item (slot or shared expert; grid-stride when there are more
-// items than waves): output rotation * svh * weight into LDS, then wave 0 sums them in slot
+// Output rotation * svh * weight of one item's summed down partials: routed slots in fp32;
+// the shared expert with the EXL3 linear's fp16 rounding points (C in fp16, fp16 svh product).
+__device__ __forceinline__ void combine_item(bool shared, float w, float s0, float s1, float (&v)[2], int lane)
+{
+    if (shared) {
+        v[0] = h2f(f2h(v[0]));
+        v[1] = h2f(f2h(v[1]));
+    }
+    had128_lane(v[0], v[1], lane);
+    if (shared) {
+        v[0] = h2f(f2h(h2f(f2h(v[0])) * s0));
+        v[1] = h2f(f2h(h2f(f2h(v[1])) * s1));
+    } else {
+        v[0] = w * (v[0] * s0);
+        v[1] = w * (v[1] * s1);
+    }
+}
+
+__device__ __forceinline__ void combine_store(const MoeParams& p, int row, int col0, int col1, float o0, float o1)
+{
+    if (p.out) {
+        float* dst = p.out + (size_t)row * p.out_stride;
+        dst[col0] = o0;
+        dst[col1] = o1;
+    }
+    if (p.residual) {
+        // h = bf16(h + bf16(y)): y cast to the activation dtype, then the bf16 add
+        uint16_t* h = p.residual + (size_t)row * p.residual_stride;
+        h[col0] = bf16_bits(bf16_value(h[col0]) + bf16_value(bf16_bits(o0)));
+        h[col1] = bf16_bits(bf16_value(h[col1]) + bf16_value(bf16_bits(o1)));
+    }
+}
+
+// Per-token reduction over slots in slot order (+ shared expert), for small batches: one
+// workgroup per (token, 128 columns) with one wave per item (slot or shared expert;
+// grid-stride when there are more items than waves) into LDS, then wave 0 sums them in slot
 // order, as the reference sums one warp per slot (exl3_moe_coop_kernel.cuh:906-940), and adds
 // the shared expert. A wave issues its item's independent loads (expert, weight, split count)
 // together, then the svh pointer and the partials, so an item costs two memory round trips.
@@ -834,19 +984,9 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
                                    : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
         float v[2];
         sum_partials(p, sk, cg, lane, ks_of_chunk(ks_down(p, units), mult), v);
-        const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
-        if (shared) {
-            v[0] = h2f(f2h(v[0]));                     // EXL3 linear C in fp16
-            v[1] = h2f(f2h(v[1]));
-        }
-        had128_lane(v[0], v[1], lane);
-        if (shared) {
-            part[k][c0] = h2f(f2h(h2f(f2h(v[0])) * s0));
-            part[k][c1] = h2f(f2h(h2f(f2h(v[1])) * s1));
-        } else {
-            part[k][c0] = w * (v[0] * s0);
-            part[k][c1] = w * (v[1] * s1);
-        }
+        combine_item(shared, w, h2f(svh[col0]), h2f(svh[col1]), v, lane);
+        part[k][c0] = v[0];
+        part[k][c1] = v[1];
         if (lane == 0) active[k] = 1;
     }
     __syncthreads();
@@ -861,18 +1001,65 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
             o0 = o0 + part[p.topk][c0];
             o1 = o1 + part[p.topk][c1];
         }
-        if (p.out) {
-            float* dst = p.out + (size_t)row * p.out_stride;
-            dst[col0] = o0;
-            dst[col1] = o1;
+        combine_store(p, row, col0, col1, o0, o1);
+    }
+}
+
+// The same reduction for large batches, where throughput matters more than the latency of one
+// token: one wave per (token, 128 columns) walks the token's items in slot order (shared expert
+// last), issuing the loads of COMBINE_BATCH items together. Same operations in the same order as
+// moe_combine_kernel, so the two give identical results.
+constexpr int COMBINE_BATCH = 4;
+
+__global__ __launch_bounds__(256) void moe_combine_rows_kernel(MoeParams p)
+{
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6));
+    const int ncg = p.H / 128;
+    if (wid >= p.T * ncg) return;
+    const int row = wid / ncg, cg = wid - row * ncg;
+    const int slots = p.T * p.topk;
+    const KSplit kd = ks_down(p, __builtin_amdgcn_readfirstlane(p.meta[2]));
+    const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
+    const int nitems = p.topk + (p.has_shared ? 1 : 0);
+    float o0 = 0.0f, o1 = 0.0f;
+    for (int b = 0; b < nitems; b += COMBINE_BATCH) {
+        int sk[COMBINE_BATCH], le[COMBINE_BATCH], S[COMBINE_BATCH];
+        float w[COMBINE_BATCH], v[COMBINE_BATCH][2], sv[COMBINE_BATCH][2];
+#pragma unroll
+        for (int j = 0; j < COMBINE_BATCH; ++j) {
+            const int k = b + j;
+            const bool shared = k == p.topk;
+            sk[j] = shared ? slots + row : row * p.topk + k;
+            le[j] = -2;                                   // -2: past the items
+            if (k < nitems) {
+                le[j] = shared ? -1 : __builtin_amdgcn_readfirstlane(p.local[sk[j]]);
+                S[j] = ks_of_chunk(kd, __builtin_amdgcn_readfirstlane(p.slot_mult[sk[j]]));
+                w[j] = shared ? 1.0f : h2f(p.rw16[sk[j]]);
+            }
         }
-        if (p.residual) {
-            // h = bf16(h + bf16(y)): y cast to the activation dtype, then the bf16 add
-            uint16_t* h = p.residual + (size_t)row * p.residual_stride;
-            h[col0] = bf16_bits(bf16_value(h[col0]) + bf16_value(bf16_bits(o0)));
-            h[col1] = bf16_bits(bf16_value(h[col1]) + bf16_value(bf16_bits(o1)));
+#pragma unroll
+        for (int j = 0; j < COMBINE_BATCH; ++j) {
+            const bool shared = b + j == p.topk;
+            if (le[j] >= 0 || (shared && le[j] == -1)) {
+                const half_t* svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
+                                           : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le[j]];
+                sum_partials(p, sk[j], cg, lane, S[j], v[j]);
+                sv[j][0] = h2f(svh[col0]);
+                sv[j][1] = h2f(svh[col1]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < COMBINE_BATCH; ++j) {
+            const bool shared = b + j == p.topk;
+            if (le[j] >= 0 || (shared && le[j] == -1)) {
+                combine_item(shared, w[j], sv[j][0], sv[j][1], v[j], lane);
+                o0 = o0 + v[j][0];
+                o1 = o1 + v[j][1];
+            }
         }
     }
+    combine_store(p, row, col0, col1, o0, o1);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -881,7 +1068,7 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
 int moe_prepare_only(MoeParams& p, hipStream_t stream)
 {
     if (p.logits) hipLaunchKernelGGL(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
-    if (p.mode & PREP_GROUP) hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, p);
+    if (p.mode & PREP_GROUP) hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64 * GROUP_WAVES), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -904,15 +1091,14 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         hipLaunchKernelGGL(moe_prepare_small_kernel, dim3(blocks), dim3(256), 0, stream, p);
     } else {
         if (p.logits) hipLaunchKernelGGL(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
-        hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, p);
+        hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64 * GROUP_WAVES), 0, stream, p);
         hipLaunchKernelGGL(moe_rotate_kernel, dim3(EVAMX_ROTATE_BLOCKS), dim3(256), 0, stream, p);
     }
     mark(1);
     if (p.mfma) {
         launch_mfma(p, 0, stream);
         mark(2);
-        const int waves = nslot * (p.I / 128);
-        hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        launch_act(p, nslot, stream);
         mark(3);
         launch_mfma(p, 1, stream);
     } else {
@@ -933,8 +1119,7 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
             }
         }
         mark(2);
-        const int waves = nslot * (p.I / 128);
-        hipLaunchKernelGGL(moe_act_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        launch_act(p, nslot, stream);
         mark(3);
         const long units = (long)EVAMX_MAX_MULT * p.max_chunks * (p.H / 128) * (p.ks_d > 0 ? p.ks_d : 1);
         const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
@@ -947,10 +1132,12 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         }
     }
     mark(4);
-    {
+    if (p.T <= EVAMX_SMALL_ROWS) {
         int nw = p.topk + (p.has_shared ? 1 : 0);
         if (nw > EVAMX_COMBINE_WAVES) nw = EVAMX_COMBINE_WAVES;
         hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(64 * nw), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(moe_combine_rows_kernel, dim3((p.T * (p.H / 128) + 3) / 4), dim3(256), 0, stream, p);
     }
     mark(5);
     return hipGetLastError() == hipSuccess ? 0 : -1;
