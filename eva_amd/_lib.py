@@ -13,7 +13,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library resolves against)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libevamx.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EVAMX_OK, EVAMX_EINVAL, EVAMX_ELAUNCH, EVAMX_ENOSPACE = 0, -1, -2, -3
 DTYPE_F16, DTYPE_BF16 = 0, 1
@@ -37,7 +37,7 @@ class MoeArgs(ctypes.Structure):
                 ("min_expert", _i32), ("max_expert", _i32), ("tables", _vp), ("k2_per_expert", _vp),
                 ("bits", _f32), ("shared", _vp), ("shared_bits", _f32), ("limit", _f32),
                 ("out", _vp), ("out_stride", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
-                ("events", _vp), ("residual", _vp), ("residual_stride", _i32)]
+                ("events", _vp), ("residual", _vp), ("residual_stride", _i32), ("gate_w", _vp)]
 
 
 class EvamxError(RuntimeError):
@@ -65,6 +65,7 @@ _SIGNATURES = {
     "evamx_moe_forward": (ctypes.c_int, [ctypes.POINTER(MoeArgs), _vp]),
     "evamx_moe_runs_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_moe_flags_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
+    "evamx_moe_logits_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_bench_decode": (ctypes.c_int, [_f32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
 }
 

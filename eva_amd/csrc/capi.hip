@@ -40,8 +40,8 @@ static bool gemv_rate(int k2) { return gemv_k2_supported(k2); }   // 1.5 .. 4, 5
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t flags, meta, local, order, runs, chunks, unit_chunk, slot_mult, rw16, xr, xsum, act, actsum, part_gu, part_d,
-        total;
+    size_t flags, meta, local, order, runs, chunks, unit_chunk, slot_mult, rw16, logits, xr, xsum, act, actsum, part_gu,
+        part_d, total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
 };
 
@@ -110,6 +110,7 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.unit_chunk = o; o = al256(o + (size_t)EVAMX_MAX_MULT * L.max_chunks * 4);
     L.slot_mult = o; o = al256(o + (size_t)L.nslot_max * 4);
     L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
+    L.logits = o;  o = al256(o + (size_t)s->rows_max * EVAMX_MAX_EXPERTS * 4);
     L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
     L.xsum = o;    o = al256(o + (size_t)2 * L.nslot_max * (s->hidden / 128) * 4);
     L.act = o;     o = al256(o + (size_t)L.nslot_max * s->inter * 2);
@@ -150,7 +151,7 @@ using namespace evamx;
 
 extern "C" const char* evamx_last_error(void) { return g_err; }
 
-extern "C" int evamx_abi_version(void) { return 2; }
+extern "C" int evamx_abi_version(void) { return 3; }
 
 extern "C" int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, float bits, void* w_fp16,
                                   evamx_stream_t stream)
@@ -260,6 +261,12 @@ extern "C" size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape)
     return moe_layout(shape).total;
 }
 
+extern "C" float* evamx_moe_logits_ptr(const evamx_moe_shape* shape, void* workspace)
+{
+    if (!shape_ok(shape) || !workspace) return nullptr;
+    return (float*)((char*)workspace + moe_layout(shape).logits);
+}
+
 extern "C" int32_t* evamx_moe_runs_ptr(const evamx_moe_shape* shape, void* workspace)
 {
     if (!shape_ok(shape) || !workspace) return nullptr;
@@ -299,7 +306,9 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
                       (!a->residual || a->residual_stride >= s->hidden),
                   "evamx_moe_forward: row strides below hidden");
     EVAMX_REQUIRE(std::isfinite(a->limit) && a->limit >= 0.0f, "evamx_moe_forward: limit must be finite and >= 0");
-    if (a->logits) {
+    EVAMX_REQUIRE(!(a->logits && a->gate_w), "evamx_moe_forward: give logits or gate_w, not both");
+    EVAMX_REQUIRE(((uintptr_t)a->gate_w & 15) == 0, "evamx_moe_forward: gate_w must be 16-byte aligned");
+    if (a->logits || a->gate_w) {
         EVAMX_REQUIRE(a->n_logits >= s->topk && a->n_logits <= EVAMX_MAX_EXPERTS,
                       "evamx_moe_forward: n_logits %d must be in topk..%d", a->n_logits, EVAMX_MAX_EXPERTS);
         EVAMX_REQUIRE(a->weights, "evamx_moe_forward: routing needs a weights output");
@@ -336,10 +345,12 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.n_logits = a->n_logits;
     p.x = a->x; p.x_dtype = a->x_dtype; p.x_stride = a->x_stride;
     p.logits = a->logits; p.sel_bias = a->sel_bias; p.score = a->score_fn; p.route_scale = a->route_scale;
+    p.gate_w = a->gate_w;
+    if (a->gate_w) p.logits = (const float*)(ws + L.logits);     // written by the gate kernel
     p.sel = a->sel;
     p.weights = a->weights;
     p.rw16 = a->rw_fp16 ? (half_t*)a->rw_fp16 : (half_t*)(ws + L.rw16);
-    if (!a->logits && !a->weights) p.weights = nullptr;    // rw_fp16 is the input
+    if (!a->logits && !a->gate_w && !a->weights) p.weights = nullptr;    // rw_fp16 is the input
     p.min_expert = a->min_expert >= 0 ? a->min_expert : -1;
     p.max_expert = a->max_expert;
     p.tables = a->tables; p.tbl_stride = s->n_local;

@@ -33,6 +33,7 @@ struct MoeParams {
     int x_dtype, x_stride;
     // routing
     const float* logits;
+    const float* gate_w;       // router front: logits = x @ gate_w^T into the workspace first (or null)
     const float* sel_bias;
     int score;
     float route_scale;

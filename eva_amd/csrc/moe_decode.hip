@@ -98,6 +98,55 @@ __device__ __forceinline__ half_t load_x16(const void* x, int dtype, size_t i)
 }
 
 // ---------------------------------------------------------------------------------------------
+// Router front: logits[r][e] = sum_k float(x[r][k]) * gate_w[e][k] in fp32 (Block.route's
+// x.float() @ gate_w.T, model.py:404-409). One wave per (expert, group of GATE_ROWS rows): lane l
+// takes k = 4l + 256j (one float4 of the weight row per step, reused by the group's rows) with a
+// sequential fma chain, and the lanes' partials meet in a fixed butterfly, so a row's logits
+// depend on that row alone whatever the batch (the per-row stable_linear of model.py:158-165).
+
+constexpr int GATE_ROWS = 8;
+
+__device__ __forceinline__ float x_at(const MoeParams& p, int r, int k)
+{
+    const uint16_t b = ((const uint16_t*)p.x)[(size_t)r * p.x_stride + k];
+    if (p.x_dtype == EVAMX_DTYPE_F16) return h2f(__builtin_bit_cast(half_t, b));
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+__global__ __launch_bounds__(256) void moe_gate_kernel(MoeParams p, float* logits)
+{
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6));
+    const int ngr = (p.T + GATE_ROWS - 1) / GATE_ROWS;
+    if (wid >= p.n_logits * ngr) return;
+    const int e = wid / ngr, r0 = (wid - e * ngr) * GATE_ROWS;
+    const float4* w = (const float4*)(p.gate_w + (size_t)e * p.H);
+    float acc[GATE_ROWS];
+#pragma unroll
+    for (int r = 0; r < GATE_ROWS; ++r) acc[r] = 0.0f;
+    for (int k4 = lane; k4 < p.H / 4; k4 += 64) {
+        const float4 wv = w[k4];
+#pragma unroll
+        for (int r = 0; r < GATE_ROWS; ++r) {
+            if (r0 + r < p.T) {
+                const int k = 4 * k4;
+                float a = acc[r];
+                a = fmaf(x_at(p, r0 + r, k + 0), wv.x, a);
+                a = fmaf(x_at(p, r0 + r, k + 1), wv.y, a);
+                a = fmaf(x_at(p, r0 + r, k + 2), wv.z, a);
+                a = fmaf(x_at(p, r0 + r, k + 3), wv.w, a);
+                acc[r] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GATE_ROWS; ++r) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && r0 + r < p.T) logits[(size_t)(r0 + r) * p.n_logits + e] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Router keys are packed as (order-preserving key bits << 32 | ~index) so that one 64-bit max, reduced
 // with lane butterflies, yields the winner and the tie rule at once (+0 and -0 compare equal).
 
@@ -1085,6 +1134,10 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     p.mfma = p.T >= EVAMX_MFMA_MIN_ROWS ? 1 : 0;
     p.chunk_rows = p.mfma ? EVAMX_TILE_ROWS : EVAMX_CHUNK;
     mark(0);
+    if (p.gate_w) {
+        const int waves = p.n_logits * ((p.T + GATE_ROWS - 1) / GATE_ROWS);
+        hipLaunchKernelGGL(moe_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, const_cast<float*>(p.logits));
+    }
     if (small) {
         int blocks = (nslot * nch * 2 + 3) / 4;
         if (blocks > 256) blocks = 256;

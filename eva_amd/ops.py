@@ -140,6 +140,12 @@ class MoeWorkspace:
         n = 2 + 2 * slots + 1
         return self.buffer[off:off + 4 * n].view(torch.int32)
 
+    def logits(self, rows: int, n_logits: int) -> torch.Tensor:
+        """fp32 ``[rows, n_logits]`` router logits the last forward computed from ``gate_w``."""
+        addr = lib().evamx_moe_logits_ptr(ctypes.byref(self.shape), ptr(self.buffer))
+        off = addr - self.buffer.data_ptr()
+        return self.buffer[off:off + 4 * rows * n_logits].view(torch.float32).view(rows, n_logits)
+
     def flags(self) -> torch.Tensor:
         addr = lib().evamx_moe_flags_ptr(ctypes.byref(self.shape), ptr(self.buffer))
         off = addr - self.buffer.data_ptr()
@@ -152,7 +158,7 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
                 weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
                 score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
                 shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0,
-                events=None, residual: torch.Tensor | None = None):
+                events=None, residual: torch.Tensor | None = None, gate_w: torch.Tensor | None = None):
     """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
 
     With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
@@ -161,6 +167,8 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     ``events``: optional ctypes array of 6 hipEvent_t handles recorded around the 5 stages.
     ``residual``: optional bf16 ``[rows, H]`` stream updated in place to ``bf16(residual + bf16(y))``
     (may be ``x`` itself); ``out`` may then be None.
+    ``gate_w``: optional fp32 ``[n_experts, H]`` router weight; the logits ``x @ gate_w.T`` are then
+    computed on the device (instead of ``logits``) and routed with ``score_fn``/``sel_bias``.
     """
     s = ws.shape
     _dev(x, "x", None, 2, row_strided=True)
@@ -184,10 +192,19 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     a.x = ptr(x)
     a.x_dtype = _lib.DTYPE_F16 if x.dtype == torch.float16 else _lib.DTYPE_BF16
     a.x_stride = x.stride(0)
-    if logits is not None:
-        _dev(logits, "logits", torch.float32, 2)
-        a.logits = ptr(logits)
-        a.n_logits = logits.shape[1]
+    if logits is not None and gate_w is not None:
+        raise ValueError("give logits or gate_w, not both")
+    if logits is not None or gate_w is not None:
+        if logits is not None:
+            _dev(logits, "logits", torch.float32, 2)
+            a.logits = ptr(logits)
+            a.n_logits = logits.shape[1]
+        else:
+            _dev(gate_w, "gate_w", torch.float32, 2)
+            if gate_w.shape[1] != s.hidden:
+                raise ValueError(f"gate_w must be [n_experts, {s.hidden}]")
+            a.gate_w = ptr(gate_w)
+            a.n_logits = gate_w.shape[0]
         a.sel_bias = ptr(sel_bias)
         a.score_fn = SCORE_FNS[score_fn]
         a.route_scale = float(route_scale)

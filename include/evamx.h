@@ -144,6 +144,11 @@ typedef struct evamx_moe_args {
      * model.py:499); may be the x of this call. NULL for none. */
     void* residual;
     int32_t residual_stride;      /* elements; >= hidden */
+    /* optional router front (Block.route's x.float() @ gate_w.T, model.py:404-409 with the
+     * per-row stable_linear of model.py:158-165): device fp32 [n_logits][hidden]; when set and
+     * logits == NULL, each row's logits are computed on the device in fp32 with a fixed
+     * reduction order (independent of the batch) and routed as above. NULL for none. */
+    const float* gate_w;
 } evamx_moe_args;
 
 size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape);
@@ -155,6 +160,10 @@ int evamx_moe_forward(const evamx_moe_args* args, evamx_stream_t stream);
  * evamx_prepare_routes with capacity = rows_max) and the sticky flag word. */
 int32_t* evamx_moe_runs_ptr(const evamx_moe_shape* shape, void* workspace);
 int32_t* evamx_moe_flags_ptr(const evamx_moe_shape* shape, void* workspace);
+/* The fp32 router logits [rows][n_logits] the last forward computed from gate_w (the router
+ * stable_linear of model.py:404-409 / stable_linear_runtime's "router" dispatch); undefined after
+ * a forward given logits. */
+float* evamx_moe_logits_ptr(const evamx_moe_shape* shape, void* workspace);
 
 /* ---- measurement --------------------------------------------------------------------------- */
 

@@ -95,6 +95,8 @@ def _args(**kw):
     (dict(limit=float("inf")), "limit"), (dict(bits=1.0), "bit rate"), (dict(bits=6.0), "bit rate"), (dict(bits=4.5), "bit rate"),
     (dict(weights=0), "weights"), (dict(min_expert=4, max_expert=4), "range"),
     (dict(logits=FAKE, n_logits=4), "n_logits"), (dict(logits=FAKE, n_logits=256, score_fn=3), "score"),
+    (dict(logits=FAKE, gate_w=FAKE, n_logits=256), "not both"), (dict(gate_w=FAKE + 4, n_logits=256), "gate_w"),
+    (dict(gate_w=FAKE, n_logits=4), "n_logits"), (dict(gate_w=FAKE, n_logits=256, weights=0), "weights"),
 ])
 def test_forward_rejects_bad_arguments(bad, msg):
     L = _lib.lib()
