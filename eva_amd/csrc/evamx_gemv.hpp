@@ -116,6 +116,20 @@ __device__ __forceinline__ void load_slice(LaneWords<K>& w, __amdgpu_buffer_rsrc
 }
 
 // ---------------------------------------------------------------------------------------------
+// Waves sharing a SIMD issue oldest-first, so without help the oldest races ahead, the youngest
+// finishes last, and the SIMD's last stretch runs one wave that cannot hide its own load
+// latency. A streaming loop sets its wave's priority from its progress (done of n steps): 3
+// below half, 2 to 3/4, 1 to 9/10, then 0, so a wave that is ahead yields to the ones behind
+// and the SIMD's waves reach each mark together; only the last tenth is issued oldest-first.
+__device__ __forceinline__ void progress_priority(int done, int n)
+{
+    if (10 * done >= 9 * n) __builtin_amdgcn_s_setprio(0);
+    else if (4 * done >= 3 * n) __builtin_amdgcn_s_setprio(1);
+    else if (2 * done >= n) __builtin_amdgcn_s_setprio(2);
+    else __builtin_amdgcn_s_setprio(3);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Rate geometry and per-slice decode of the lane layout (lane = 8*i + q owns tile i's columns q
 // and q + 8 for the 16 k of a k-slice), shared by the decode GEMV and the MFMA path.
 
@@ -294,25 +308,14 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // Waves sharing a SIMD issue oldest-first, so without help the oldest races ahead, the
-    // youngest finishes last, and the SIMD's last stretch runs one wave that cannot hide its
-    // own load latency. Priority falls with progress (3 below half the range, 2 to 3/4, 1 to
-    // 9/10, then 0), so a wave that is ahead yields to the ones behind and the SIMD's waves
-    // reach each mark together; only the last tenth is issued oldest-first.
     const int n_kt = kt1 - kt0;
-    auto set_priority = [&](int done) {
-        if (10 * done >= 9 * n_kt) __builtin_amdgcn_s_setprio(0);
-        else if (4 * done >= 3 * n_kt) __builtin_amdgcn_s_setprio(1);
-        else if (2 * done >= n_kt) __builtin_amdgcn_s_setprio(2);
-        else __builtin_amdgcn_s_setprio(3);
-    };
     int kt = kt0;
     for (; kt + PF <= kt1; kt += PF) {
-        set_priority(kt - kt0);
+        progress_priority(kt - kt0, n_kt);
 #pragma unroll
         for (int d = 0; d < PF; ++d) step(kt + d, ring[d]);
     }
-    set_priority(n_kt);
+    progress_priority(n_kt, n_kt);
 #pragma unroll
     for (int d = 0; d < PF - 1; ++d)
         if (kt + d < kt1) step(kt + d, ring[d]);

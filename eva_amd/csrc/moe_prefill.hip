@@ -43,7 +43,7 @@ __device__ __forceinline__ void wave_lds_fence()
 // with 128-chunk sums) times the decoded weights of tiles 8*cg .. 8*cg+7 of a projection over
 // the k-slices [kt0, kt1) (whole 128-chunks); writes part[slot * part_stride + 128 * cg +
 // column] for rows < rows.
-template <int K2, int MB>
+template <int K2, int MB, bool PRIO>
 __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
                                           const GlobalRows& src, const int* __restrict__ slot_of, int rows,
                                           float* __restrict__ part, size_t part_stride, uint32_t* lds)
@@ -130,9 +130,11 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
 
     // nk is a multiple of 8 (whole 128-chunks): pairs of ring slots per step, two steps per round
     for (int kk = 0; kk < (nk >> 1); kk += 2) {
+        if constexpr (PRIO) progress_priority(kk, nk >> 1);
         kstep(kk, ring[0], ring[1]);
         kstep(kk + 1, ring[2], ring[3]);
     }
+    if constexpr (PRIO) progress_priority(1, 1);
 
     // activation sums of the rows over the item's chunks: lane (m16, g) sums chunks c0 + g,
     // c0 + g + 4, ... of row m16 + 16 mb; the four k groups are summed across lanes; then each
@@ -170,15 +172,17 @@ __device__ __forceinline__ void mfma_item_rows(const uint32_t* trellis, int nt_n
                                                const GlobalRows& src, const int* slot_of, int rows, float* part,
                                                size_t part_stride, uint32_t* lds)
 {
+    // equal-length items of one 16-row block (calls of at most 16 tokens) gain from progress
+    // priorities (3 waves per SIMD); the prefill kernel's items differ in rows and gain nothing
     if constexpr (MBMAX == 1) {
-        mfma_item<K2, 1>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds);
+        mfma_item<K2, 1, true>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds);
     } else {
         const int mb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
         switch (mb) {
-            case 1: mfma_item<K2, 1>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-            case 2: mfma_item<K2, 2>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-            case 3: mfma_item<K2, 3>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-            default: mfma_item<K2, 4>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 1: mfma_item<K2, 1, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 2: mfma_item<K2, 2, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 3: mfma_item<K2, 3, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            default: mfma_item<K2, 4, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
         }
     }
 }
