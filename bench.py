@@ -374,7 +374,7 @@ def run_layer(torch, args):
         if prefill:
             result["cpu_baseline"] = cpu_baseline(bits=4.0, tokens=16, n_routed=1)
         else:
-            result["cpu_baseline"] = cpu_baseline(bits=args.bits, tokens=1, n_routed=1)
+            result["cpu_baseline"] = cpu_baseline(bits=args.bits, tokens=T, n_routed=1)
     return result
 
 
@@ -520,10 +520,11 @@ def measured_traffic(tokens, bits):
 
 
 def kernel_times(torch, stream, step, n, skip):
-    """Average duration of each of the five stages, from hipEvents recorded between the launches
-    on the launch stream (eager calls step(i, events))."""
+    """Average duration of each of the five stages, from the start timestamp of a stage's first
+    kernel to the end timestamp of its last (events taken by the kernel launches themselves on
+    the launch stream; eager calls step(i, events))."""
     names = ["moe_prepare", "moe_gate_up", "moe_act", "moe_down", "moe_combine"]
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(n)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(10)] for _ in range(n)]
     for row in evs:
         for e in row:
             e.record(stream)          # creates the underlying hipEvent
@@ -531,14 +532,14 @@ def kernel_times(torch, stream, step, n, skip):
     handles = []
     with torch.cuda.stream(stream):
         for i in range(n):
-            hs = (ctypes.c_void_p * 6)(*[e.cuda_event for e in evs[i]])
+            hs = (ctypes.c_void_p * 10)(*[e.cuda_event for e in evs[i]])
             handles.append(hs)
             step(i, events=hs)
     torch.cuda.synchronize()
     acc = [0.0] * 5
     for i in range(skip, n):
         for k in range(5):
-            acc[k] += evs[i][k].elapsed_time(evs[i][k + 1])
+            acc[k] += evs[i][2 * k].elapsed_time(evs[i][2 * k + 1])
     return {names[k]: acc[k] * 1e3 / (n - skip) for k in range(5)}
 
 

@@ -3,6 +3,7 @@
 #pragma once
 #include <stdint.h>
 #include "../../include/evamx.h"
+#include <hip/hip_ext.h>
 #include "evamx_device.hpp"
 
 namespace evamx {
@@ -131,7 +132,19 @@ __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
 __host__ __device__ __forceinline__ int chunk_rows_of(const MoeParams& p) { return p.chunk_rows > 0 ? p.chunk_rows : EVAMX_CHUNK; }
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);
-int launch_mfma(const MoeParams& p, int which, hipStream_t stream);
+// Kernel launch that, given events, records the kernel's own start and end timestamps in them
+// (hipExtLaunchKernel), as a profiler's kernel trace reports them; plain launch otherwise.
+template <typename... KArgs, typename... Args>
+inline void launch_timed(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream, hipEvent_t start,
+                         hipEvent_t stop, Args... args)
+{
+    if (start || stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+}
+
+int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 int moe_prepare_only(MoeParams& p, hipStream_t stream);
 bool moe_small_path(int T, int topk);
 

@@ -898,15 +898,15 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
 
 // Activation launch: one wave per (row, chunk) for small batches (latency), per (row, 4 chunks)
 // for large ones (the row's slot, expert and pointers resolved once).
-static void launch_act(const MoeParams& p, int nslot, hipStream_t stream)
+static void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
 {
     const int na = p.I / 128;
     if (p.T > EVAMX_SMALL_ROWS && na % 4 == 0) {
         const int waves = nslot * (na / 4);
-        hipLaunchKernelGGL(moe_act_kernel<4>, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        launch_timed(moe_act_kernel<4>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
     } else {
         const int waves = nslot * na;
-        hipLaunchKernelGGL(moe_act_kernel<1>, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        launch_timed(moe_act_kernel<1>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
     }
 }
 
@@ -1125,35 +1125,36 @@ bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
 {
-    auto mark = [&](int i) {
-        if (events) (void)hipEventRecord((hipEvent_t)events[i], stream);
-    };
+    // events[2k] / events[2k + 1]: start of the first and end of the last kernel of stage k
+    auto ev = [&](int i) { return events ? (hipEvent_t)events[i] : (hipEvent_t) nullptr; };
     const int nch = p.H / 128;
     const int nslot = p.T * p.topk + (p.has_shared ? p.T : 0);
     const bool small = moe_small_path(p.T, p.topk);
     p.mfma = p.T >= EVAMX_MFMA_MIN_ROWS ? 1 : 0;
     p.chunk_rows = p.mfma ? EVAMX_TILE_ROWS : EVAMX_CHUNK;
-    mark(0);
+    hipEvent_t first = ev(0);
     if (p.gate_w) {
         const int waves = p.n_logits * ((p.T + GATE_ROWS - 1) / GATE_ROWS);
-        hipLaunchKernelGGL(moe_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, const_cast<float*>(p.logits));
+        launch_timed(moe_gate_kernel, dim3((waves + 3) / 4), dim3(256), stream, first, nullptr, p,
+                     const_cast<float*>(p.logits));
+        first = nullptr;
     }
     if (small) {
         int blocks = (nslot * nch * 2 + 3) / 4;
         if (blocks > 256) blocks = 256;
-        hipLaunchKernelGGL(moe_prepare_small_kernel, dim3(blocks), dim3(256), 0, stream, p);
+        launch_timed(moe_prepare_small_kernel, dim3(blocks), dim3(256), stream, first, ev(1), p);
     } else {
-        if (p.logits) hipLaunchKernelGGL(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
-        hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64 * GROUP_WAVES), 0, stream, p);
-        hipLaunchKernelGGL(moe_rotate_kernel, dim3(EVAMX_ROTATE_BLOCKS), dim3(256), 0, stream, p);
+        if (p.logits) {
+            launch_timed(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), stream, first, nullptr, p);
+            first = nullptr;
+        }
+        launch_timed(moe_group_kernel, dim3(1), dim3(64 * GROUP_WAVES), stream, first, nullptr, p);
+        launch_timed(moe_rotate_kernel, dim3(EVAMX_ROTATE_BLOCKS), dim3(256), stream, nullptr, ev(1), p);
     }
-    mark(1);
     if (p.mfma) {
-        launch_mfma(p, 0, stream);
-        mark(2);
-        launch_act(p, nslot, stream);
-        mark(3);
-        launch_mfma(p, 1, stream);
+        launch_mfma(p, 0, stream, ev(2), ev(3));
+        launch_act(p, nslot, stream, ev(4), ev(5));
+        launch_mfma(p, 1, stream, ev(6), ev(7));
     } else {
         // Chunks hold at most min(T, EVAMX_CHUNK) rows: each token picks an expert once, and the
         // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
@@ -1165,34 +1166,30 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
             const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
             const half_t* xr = p.xr;
             switch (tmax) {
-                case 1: hipLaunchKernelGGL(moe_gate_up_kernel<1>, grid, dim3(256), 0, stream, p, xr); break;
-                case 2: hipLaunchKernelGGL(moe_gate_up_kernel<2>, grid, dim3(256), 0, stream, p, xr); break;
-                case 4: hipLaunchKernelGGL(moe_gate_up_kernel<4>, grid, dim3(256), 0, stream, p, xr); break;
-                default: hipLaunchKernelGGL(moe_gate_up_kernel<8>, grid, dim3(256), 0, stream, p, xr); break;
+                case 1: launch_timed(moe_gate_up_kernel<1>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
+                case 2: launch_timed(moe_gate_up_kernel<2>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
+                case 4: launch_timed(moe_gate_up_kernel<4>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
+                default: launch_timed(moe_gate_up_kernel<8>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
             }
         }
-        mark(2);
-        launch_act(p, nslot, stream);
-        mark(3);
+        launch_act(p, nslot, stream, ev(4), ev(5));
         const long units = (long)EVAMX_MAX_MULT * p.max_chunks * (p.H / 128) * (p.ks_d > 0 ? p.ks_d : 1);
         const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
         const half_t* act = p.act;
         switch (tmax) {
-            case 1: hipLaunchKernelGGL(moe_down_kernel<1>, grid, dim3(256), 0, stream, p, act); break;
-            case 2: hipLaunchKernelGGL(moe_down_kernel<2>, grid, dim3(256), 0, stream, p, act); break;
-            case 4: hipLaunchKernelGGL(moe_down_kernel<4>, grid, dim3(256), 0, stream, p, act); break;
-            default: hipLaunchKernelGGL(moe_down_kernel<8>, grid, dim3(256), 0, stream, p, act); break;
+            case 1: launch_timed(moe_down_kernel<1>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
+            case 2: launch_timed(moe_down_kernel<2>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
+            case 4: launch_timed(moe_down_kernel<4>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
+            default: launch_timed(moe_down_kernel<8>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
         }
     }
-    mark(4);
     if (p.T <= EVAMX_SMALL_ROWS) {
         int nw = p.topk + (p.has_shared ? 1 : 0);
         if (nw > EVAMX_COMBINE_WAVES) nw = EVAMX_COMBINE_WAVES;
-        hipLaunchKernelGGL(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(64 * nw), 0, stream, p);
+        launch_timed(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(64 * nw), stream, ev(8), ev(9), p);
     } else {
-        hipLaunchKernelGGL(moe_combine_rows_kernel, dim3((p.T * (p.H / 128) + 3) / 4), dim3(256), 0, stream, p);
+        launch_timed(moe_combine_rows_kernel, dim3((p.T * (p.H / 128) + 3) / 4), dim3(256), stream, ev(8), ev(9), p);
     }
-    mark(5);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

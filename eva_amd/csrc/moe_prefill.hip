@@ -276,7 +276,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(M
 
 // Launch of one projection stage: enough workgroups for the largest possible item count (the
 // workspace's tile bound times the largest split); workgroups past the call's items exit at once.
-int launch_mfma(const MoeParams& p, int which, hipStream_t stream)
+int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
 {
     const int ncg = which == 0 ? p.I / 128 : p.H / 128;
     const int kreq = which == 0 ? p.ks_gu : p.ks_d;
@@ -289,9 +289,9 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream)
     long blocks = (items + MF_WAVES - 1) / MF_WAVES;
     blocks = (blocks + 7) & ~7L;
     if (p.T <= 16)
-        hipLaunchKernelGGL(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), 0, stream, p, which);
+        launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
     else
-        hipLaunchKernelGGL(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), 0, stream, p, which);
+        launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -164,7 +164,8 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
     must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
     the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
-    ``events``: optional ctypes array of 6 hipEvent_t handles recorded around the 5 stages.
+    ``events``: optional ctypes array of 10 hipEvent_t handles: start and end timestamps of the
+    5 stages' kernels (prepare, gate/up, activation, down, combine).
     ``residual``: optional bf16 ``[rows, H]`` stream updated in place to ``bf16(residual + bf16(y))``
     (may be ``x`` itself); ``out`` may then be None.
     ``gate_w``: optional fp32 ``[n_experts, H]`` router weight; the logits ``x @ gate_w.T`` are then

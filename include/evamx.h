@@ -135,9 +135,10 @@ typedef struct evamx_moe_args {
     int32_t out_stride;           /* elements; >= hidden */
     void* workspace;              /* device, evamx_moe_workspace_bytes(&shape) bytes */
     size_t workspace_bytes;
-    /* optional: 6 hipEvent_t recorded on the launch stream around the 5 stages (prepare,
-     * gate/up GEMV, activation, down GEMV, combine): events[i] before stage i, events[5]
-     * after the last; NULL for none */
+    /* optional: 10 hipEvent_t for the 5 stages (prepare, gate/up, activation, down,
+     * combine): events[2k] takes the start timestamp of stage k's first kernel and
+     * events[2k+1] the end timestamp of its last (kernel timestamps, hipExtLaunchKernel);
+     * NULL for none */
     void* const* events;
     /* optional residual stream: bf16 [rows][residual_stride], updated in place to
      * bf16(residual + bf16(out)) (the layer output cast to the activation dtype and added,
