@@ -334,6 +334,24 @@ __device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lane)
     }
 }
 
+// Activity of one slot (exl3_moe_coop_kernel.cuh:208-223): its local expert, or -1 when its fp16
+// weight is zero, its expert is outside [min_expert, max_expert), or the local index is out of
+// bounds (which also sets the sticky flag when flag is set).
+__device__ __forceinline__ int slot_local(const MoeParams& p, int64_t e, half_t rw, bool flag)
+{
+    if (h2f(rw) == 0.0f) return -1;
+    int64_t le = e;
+    if (p.min_expert >= 0) {
+        if (!(e >= p.min_expert && e < p.max_expert)) return -1;
+        le = e - p.min_expert;
+    }
+    if (le < 0 || le >= p.n_local) {
+        if (flag) atomicOr(p.err, EVAMX_ERR_EXPERT_RANGE);
+        return -1;
+    }
+    return (int)le;
+}
+
 // Slot activity (exl3_moe_coop_kernel.cuh:208-223) -> local[s] = local expert or -1 (bounds
 // violations set the sticky flag and make the slot inactive), then the stable order of the
 // active slots by (expert, slot) and, when publishing, the reference run table.
@@ -346,22 +364,7 @@ __device__ void group_slots(const MoeParams& p, const SelT* sel, const half_t* r
     for (int e = t; e < E; e += nt) { ex.cnt[e] = 0; ex.fill[e] = 0; }
     __syncthreads();
     for (int s = t; s < slots; s += nt) {
-        const int64_t e = (int64_t)sel[s];
-        const float w = h2f(rw[s]);
-        int lo = -1;
-        if (w != 0.0f) {
-            int64_t le = e;
-            bool ok = true;
-            if (p.min_expert >= 0) {
-                ok = e >= p.min_expert && e < p.max_expert;
-                le = e - p.min_expert;
-            }
-            if (ok) {
-                if (le < 0 || le >= E) {
-                    if (publish) atomicOr(p.err, EVAMX_ERR_EXPERT_RANGE);
-                } else lo = (int)le;
-            }
-        }
+        const int lo = slot_local(p, (int64_t)sel[s], rw[s], publish);
         local[s] = lo;
         if (lo >= 0) atomicAdd(&ex.cnt[lo], 1);
     }
@@ -617,7 +620,8 @@ __device__ void rotate_chunks(const MoeParams& p, int s, int e, int proj, int c0
     }
 }
 
-// Rotations of n_rows grouped rows by the waves [w0, w0 + nw) of the grid.
+// Rotations of n_rows rows by the waves [w0, w0 + nw) of the grid: grouped rows order[0..n_rows),
+// or, with order null, slots 0..n_rows (routed slots then shared rows; inactive slots skipped).
 __device__ void rotate_rows(const MoeParams& p, const int* order, const int* local, int n_rows, int w, int nw, int lane)
 {
     const int nch = p.H / 128;
@@ -629,15 +633,17 @@ __device__ void rotate_rows(const MoeParams& p, const int* order, const int* loc
     for (int it = w; it < units * parts; it += nw) {
         const int u = it / parts, part = it - u * parts;
         const int o = u >> 1, proj = u & 1;
-        const int s = __builtin_amdgcn_readfirstlane(order[o]);
+        const int s = order ? __builtin_amdgcn_readfirstlane(order[o]) : o;
         const int e = s < slots ? __builtin_amdgcn_readfirstlane(local[s]) : -1;
+        if (s < slots && e < 0) continue;                 // inactive slot (slot enumeration only)
         rotate_chunks(p, s, e, proj, nch * part / parts, nch * (part + 1) / parts, lane);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Prepare for small batches (T*topk <= EVAMX_SMALL_SLOTS, T <= EVAMX_SMALL_ROWS): every
-// workgroup routes and groups in LDS, workgroup 0 publishes, then all workgroups rotate.
+// workgroup routes in LDS; workgroup 0 groups the slots and publishes the tables while the
+// others rotate the active slots' inputs (rotations are stored by slot, so they need no order).
 
 constexpr int EVAMX_SMALL_SLOTS = 512;
 constexpr int EVAMX_SMALL_ROWS = 16;
@@ -672,12 +678,20 @@ __global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
         for (int i = t; i < table_len; i += 256) p.runs[i] = 0;
     }
     __syncthreads();
+    if (!pub) {
+        // rotation workgroups need only each slot's expert: the grouping is workgroup 0's
+        for (int s = t; s < slots; s += 256) sh.local[s] = slot_local(p, sh.sel[s], sh.rw[s], false);
+        __syncthreads();
+        rotate_rows(p, nullptr, sh.local, slots + (p.has_shared ? p.T : 0), (blockIdx.x - 1) * 4 + wave,
+                    (gridDim.x - 1) * 4, lane);
+        return;
+    }
     group_slots(p, sh.sel, sh.rw, slots, sh.local, sh.order, sh.ex, pub);
     const int n_active = sh.ex.off[p.n_local];
     if (p.has_shared)
         for (int r = t; r < p.T; r += 256) sh.order[n_active + r] = slots + r;
     __syncthreads();
-    if (pub) {
+    {
         for (int s = t; s < slots; s += 256) p.local[s] = sh.local[s];
         for (int i = t; i < n_active + (p.has_shared ? p.T : 0); i += 256) p.order[i] = sh.order[i];
         write_chunks(p, sh.ex, sh.order);
@@ -690,7 +704,6 @@ __global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
             p.meta[2] = total_units(p, sh.ex);
         }
     }
-    rotate_rows(p, sh.order, sh.local, n_active + (p.has_shared ? p.T : 0), blockIdx.x * 4 + wave, gridDim.x * 4, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1140,8 +1153,8 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         first = nullptr;
     }
     if (small) {
-        int blocks = (nslot * nch * 2 + 3) / 4;
-        if (blocks > 256) blocks = 256;
+        int blocks = 1 + (nslot * nch * 2 + 3) / 4;      // workgroup 0 groups, the others rotate
+        if (blocks > 257) blocks = 257;
         launch_timed(moe_prepare_small_kernel, dim3(blocks), dim3(256), stream, first, ev(1), p);
     } else {
         if (p.logits) {
