@@ -642,8 +642,9 @@ __device__ void rotate_rows(const MoeParams& p, const int* order, const int* loc
 
 // ---------------------------------------------------------------------------------------------
 // Prepare for small batches (T*topk <= EVAMX_SMALL_SLOTS, T <= EVAMX_SMALL_ROWS): every
-// workgroup routes in LDS; workgroup 0 groups the slots and publishes the tables while the
-// others rotate the active slots' inputs (rotations are stored by slot, so they need no order).
+// workgroup routes in LDS, one wave per token (workgroups of max(4, T) waves); workgroup 0
+// groups the slots and publishes the tables while the others rotate the active slots' inputs
+// (rotations are stored by slot, so they need no order).
 
 constexpr int EVAMX_SMALL_SLOTS = 512;
 constexpr int EVAMX_SMALL_ROWS = 16;
@@ -656,16 +657,16 @@ struct SmallLds {
     int order[EVAMX_SMALL_SLOTS + EVAMX_SMALL_ROWS];
 };
 
-__global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
+__global__ __launch_bounds__(64 * EVAMX_SMALL_ROWS) void moe_prepare_small_kernel(MoeParams p)
 {
     __shared__ SmallLds sh;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, nwv = nt >> 6;
     const int slots = p.T * p.topk;
     const bool pub = blockIdx.x == 0;
     if (p.logits) {
-        for (int r = wave; r < p.T; r += 4) route_token(p, r, lane, sh.sel, sh.rw, pub);
+        for (int r = wave; r < p.T; r += nwv) route_token(p, r, lane, sh.sel, sh.rw, pub);
     } else {
-        for (int s = t; s < slots; s += 256) {
+        for (int s = t; s < slots; s += nt) {
             const int64_t e = p.sel[s];
             // indices outside the int range are outside any table: keep them out of range
             sh.sel[s] = (e >= 0 && e < 0x7fffffff) ? (int)e : -1;
@@ -675,25 +676,25 @@ __global__ __launch_bounds__(256) void moe_prepare_small_kernel(MoeParams p)
     }
     if (pub && p.runs) {
         const int table_len = 2 + 2 * p.slots_max + 1;
-        for (int i = t; i < table_len; i += 256) p.runs[i] = 0;
+        for (int i = t; i < table_len; i += nt) p.runs[i] = 0;
     }
     __syncthreads();
     if (!pub) {
         // rotation workgroups need only each slot's expert: the grouping is workgroup 0's
-        for (int s = t; s < slots; s += 256) sh.local[s] = slot_local(p, sh.sel[s], sh.rw[s], false);
+        for (int s = t; s < slots; s += nt) sh.local[s] = slot_local(p, sh.sel[s], sh.rw[s], false);
         __syncthreads();
-        rotate_rows(p, nullptr, sh.local, slots + (p.has_shared ? p.T : 0), (blockIdx.x - 1) * 4 + wave,
-                    (gridDim.x - 1) * 4, lane);
+        rotate_rows(p, nullptr, sh.local, slots + (p.has_shared ? p.T : 0), (blockIdx.x - 1) * nwv + wave,
+                    (gridDim.x - 1) * nwv, lane);
         return;
     }
     group_slots(p, sh.sel, sh.rw, slots, sh.local, sh.order, sh.ex, pub);
     const int n_active = sh.ex.off[p.n_local];
     if (p.has_shared)
-        for (int r = t; r < p.T; r += 256) sh.order[n_active + r] = slots + r;
+        for (int r = t; r < p.T; r += nt) sh.order[n_active + r] = slots + r;
     __syncthreads();
     {
-        for (int s = t; s < slots; s += 256) p.local[s] = sh.local[s];
-        for (int i = t; i < n_active + (p.has_shared ? p.T : 0); i += 256) p.order[i] = sh.order[i];
+        for (int s = t; s < slots; s += nt) p.local[s] = sh.local[s];
+        for (int i = t; i < n_active + (p.has_shared ? p.T : 0); i += nt) p.order[i] = sh.order[i];
         write_chunks(p, sh.ex, sh.order);
         if (t == 0) {
             p.runs[0] = sh.ex.run_base[p.n_local];
@@ -1153,9 +1154,11 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         first = nullptr;
     }
     if (small) {
-        int blocks = 1 + (nslot * nch * 2 + 3) / 4;      // workgroup 0 groups, the others rotate
+        // workgroup 0 groups, the others rotate; a wave per token routes in every workgroup
+        const int nwv = p.T > 4 ? p.T : 4;
+        int blocks = 1 + (nslot * nch * 2 + nwv - 1) / nwv;
         if (blocks > 257) blocks = 257;
-        launch_timed(moe_prepare_small_kernel, dim3(blocks), dim3(256), stream, first, ev(1), p);
+        launch_timed(moe_prepare_small_kernel, dim3(blocks), dim3(64 * nwv), stream, first, ev(1), p);
     } else {
         if (p.logits) {
             launch_timed(moe_route_kernel, dim3((p.T + 3) / 4), dim3(256), stream, first, nullptr, p);
