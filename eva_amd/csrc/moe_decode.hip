@@ -1155,9 +1155,11 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     }
     if (small) {
         // workgroup 0 groups, the others rotate; a wave per token routes in every workgroup
+        // at most one workgroup per CU (gemv_waves = 16 per CU), so that none waits for a slot
         const int nwv = p.T > 4 ? p.T : 4;
+        const int cus = p.gemv_waves / 16 > 2 ? p.gemv_waves / 16 : 2;
         int blocks = 1 + (nslot * nch * 2 + nwv - 1) / nwv;
-        if (blocks > 257) blocks = 257;
+        if (blocks > cus) blocks = cus;
         launch_timed(moe_prepare_small_kernel, dim3(blocks), dim3(64 * nwv), stream, first, ev(1), p);
     } else {
         if (p.logits) {
