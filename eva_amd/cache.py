@@ -13,9 +13,9 @@ the pointer tables never change: there is no ``_flush`` before a call, no routes
 can be captured into a hipGraph. Rates come from the pack per expert (mixed-rate packs work);
 ``k``, when given, must match them.
 
-``moe_step`` is the fused form a decode step uses: routing from gate logits on the device
-(``Block.route``, model.py:404-416), the routed experts, and optionally the shared expert
-(``Block._shared``, model.py:418-452, added at model.py:498).
+``moe_step`` is the fused form a decode step uses: routing on the device from gate logits or
+from the router weight itself (``Block.route``, model.py:404-416), the routed experts, and
+optionally the shared expert (``Block._shared``, model.py:418-452, added at model.py:498).
 """
 from __future__ import annotations
 
@@ -95,12 +95,14 @@ class ResidentExperts:
         ops.moe_forward(ws, x2.contiguous(), table, out, limit=float(limit), k2_per_expert=k2, sel=sel, weights=w)
         return out
 
-    def moe_step(self, layer, x, logits, *, limit=0.0, score_fn="sigmoid", sel_bias=None, route_scale=1.0,
-                 shared=None, shared_bits=None, residual=None, out=None, sel=None, weights=None):
-        """Route on the device from fp32 ``logits [rows, n_experts]`` and run the routed experts plus,
-        when ``shared`` (9 device pointers) is given, the shared expert. With ``residual`` (bf16
-        ``[rows, hidden]``, may be ``x``) the output is added into it in place. Returns
-        ``(out, sel, weights)``; capturable into a hipGraph (no host synchronisation)."""
+    def moe_step(self, layer, x, logits=None, *, gate_w=None, limit=0.0, score_fn="sigmoid", sel_bias=None,
+                 route_scale=1.0, shared=None, shared_bits=None, residual=None, out=None, sel=None, weights=None):
+        """Route on the device from fp32 ``logits [rows, n_experts]``, or from the router weight
+        ``gate_w`` (fp32 ``[n_experts, hidden]``: the logits ``x.float() @ gate_w.T`` are computed
+        in the same call, model.py:404-409), and run the routed experts plus, when ``shared``
+        (9 device pointers) is given, the shared expert. With ``residual`` (bf16 ``[rows, hidden]``,
+        may be ``x``) the output is added into it in place. Returns ``(out, sel, weights)``;
+        capturable into a hipGraph (no host synchronisation)."""
         self._check(x, None, None)
         table, k2 = self._layer(layer)
         rows = x.shape[0]
@@ -111,8 +113,10 @@ class ResidentExperts:
             weights = torch.empty(rows, self.topk, dtype=torch.float32, device=self.device)
         if out is None and residual is None:
             out = torch.empty(rows, self.hidden, dtype=torch.float32, device=self.device)
-        ops.moe_forward(ws, x, table, out, limit=float(limit), k2_per_expert=k2, logits=logits, sel=sel,
-                        weights=weights, score_fn=score_fn, sel_bias=sel_bias, route_scale=route_scale,
+        if (logits is None) == (gate_w is None):
+            raise ValueError("give logits or gate_w")
+        ops.moe_forward(ws, x, table, out, limit=float(limit), k2_per_expert=k2, logits=logits, gate_w=gate_w,
+                        sel=sel, weights=weights, score_fn=score_fn, sel_bias=sel_bias, route_scale=route_scale,
                         shared_ptrs=shared, shared_bits=shared_bits, residual=residual)
         return out, sel, weights
 

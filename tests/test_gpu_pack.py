@@ -67,3 +67,23 @@ def test_resident_store_matches_oracle(dev, tmp_path):
     assert np.array_equal(sel.cpu().numpy(), idx2)
     assert rel_err_rows(out.cpu().numpy(), ref2) < TOL
     assert store.flags(topk, True) == 0
+
+    # the same step routed from the router weight: the routes are the oracle's routes of the
+    # logits the kernel computed, into a residual stream updated in place
+    gate_w = (rng.standard_normal((8, H)) / np.sqrt(H)).astype(np.float32)
+    h0 = synth.activations_bf16(rng, T, H)
+    h = to_dev(h0, dev).to(torch.bfloat16)
+    _, sel3, _ = store.moe_step(0, h.clone(), gate_w=to_dev(gate_w, dev), limit=limit, shared=ds.ptrs(0),
+                                shared_bits=4.0, residual=h, score_fn="sqrt_softplus")
+    torch.cuda.synchronize()
+    z = store._ws[(topk, True)].logits(T, 8).cpu().numpy().copy()
+    ref3, idx3, _, _ = coop.moe_layer(h0, z, oracle_layers[0], shared, topk, limit,
+                                      score_fn="sqrt_softplus")
+    assert np.array_equal(sel3.cpu().numpy(), idx3)
+    want = coop.residual_add(h0, ref3)
+    got = h.float().cpu().numpy()
+    # one bf16 rounding of the sum, plus the layer tolerance on the layer's contribution
+    bound = np.maximum(np.abs(want), np.abs(got)) * 2.0 ** -8 + TOL * np.abs(ref3).max()
+    assert np.all(np.abs(got - want) <= bound)
+    with pytest.raises(ValueError):
+        store.moe_step(0, h, to_dev(logits, dev), gate_w=to_dev(gate_w, dev))
