@@ -40,7 +40,7 @@ static bool gemv_rate(int k2) { return gemv_k2_supported(k2); }   // 1.5 .. 4, 5
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t flags, meta, local, order, runs, chunks, unit_chunk, slot_mult, rw16, logits, xr, xsum, act, actsum, part_gu,
+    size_t flags, meta, local, order, runs, chunks, unit_chunk, tiles, slot_mult, rw16, logits, xr, xsum, act, actsum, part_gu,
         part_d, total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
 };
@@ -108,6 +108,7 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.runs = o;    o = al256(o + (size_t)(2 + 2 * L.slots_max + 1) * 4);
     L.chunks = o;  o = al256(o + (size_t)L.max_chunks * 32);
     L.unit_chunk = o; o = al256(o + (size_t)EVAMX_MAX_MULT * L.max_chunks * 4);
+    L.tiles = o;   o = al256(o + (size_t)L.max_chunks * 4);
     L.slot_mult = o; o = al256(o + (size_t)L.nslot_max * 4);
     L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
     L.logits = o;  o = al256(o + (size_t)s->rows_max * EVAMX_MAX_EXPERTS * 4);
@@ -367,6 +368,7 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.slots_max = L.slots_max;
     p.chunks = (int*)(ws + L.chunks);
     p.unit_chunk = (int*)(ws + L.unit_chunk);
+    p.tiles = (int*)(ws + L.tiles);
     p.slot_mult = (int*)(ws + L.slot_mult);
     p.max_chunks = L.max_chunks;
     p.xr = (half_t*)(ws + L.xr);

@@ -60,8 +60,12 @@ struct MoeParams {
                                // units (cost weight of the chunk, chunk_mult), 0, 0
     int max_chunks;
     int* unit_chunk;           // [EVAMX_MAX_MULT * max_chunks]: work unit -> chunk
+    int* tiles;                // [max_chunks] MFMA tiles by size, each class in expert order: those
+                               // of at most 16 rows from the front (meta[3] of them), the rest from
+                               // the back
     int* slot_mult;            // [nslot_max]: cost weight of the chunk holding each slot/shared row
-    int* meta;                 // [0] n_chunks, [1] n_active, [2] n_units
+    int* meta;                 // [0] n_chunks, [1] n_active, [2] n_units, [3] MFMA tiles of at
+                               // most 16 rows
     half_t* xr;                // [2][nslot_max][H] rotated gate/up inputs
     float* xsum;               // [2][nslot_max][H/128] their 128-chunk sums
     half_t* act;               // [nslot_max][I] rotated down inputs

@@ -274,6 +274,8 @@ struct ExpertLds {
     int chunk_base[EVAMX_MAX_EXPERTS + 1];
     int unit_base[EVAMX_MAX_EXPERTS + 1];
     int fill[EVAMX_MAX_EXPERTS];
+    int small_base[EVAMX_MAX_EXPERTS + 1];   // MFMA tiles of at most 16 rows
+    int large_base[EVAMX_MAX_EXPERTS + 1];   // MFMA tiles of more than 16 rows
 };
 
 // Work units (summed chunk weights) of an expert with n active slots.
@@ -299,15 +301,16 @@ __device__ __forceinline__ int wave_incl_scan(int v)
 
 // Per-expert offsets by one wave, from the slot counts cnt[0..E): exclusive prefix sums of the
 // counts (off), of the 8-slot runs (run_base), of the chunks of chunk_rows_of(p) slots
-// (chunk_base) and of the GEMV work units (unit_base), each with its total at [E]. Lane l owns
-// experts PER*l .. PER*l + PER-1 in registers; the four lane-total scans run together.
+// (chunk_base), of the GEMV work units (unit_base) and, for the MFMA path, of the tiles of at most
+// and of more than 16 rows (small_base, large_base), each with its total at [E]. Lane l owns
+// experts PER*l .. PER*l + PER-1 in registers; the six lane-total scans run together.
 template <int PER>
 __device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lane)
 {
     const int E = p.n_local;
     const int cs = 31 - __builtin_clz(chunk_rows_of(p));      // chunk rows are a power of two
     const int e0 = lane * PER;
-    int v[4][PER], tot[4] = {0, 0, 0, 0};
+    int v[6][PER], tot[6] = {0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int n = e0 + i < E ? ex.cnt[e0 + i] : 0;
@@ -315,15 +318,19 @@ __device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lane)
         v[1][i] = (n + 7) >> 3;
         v[2][i] = (n + (1 << cs) - 1) >> cs;
         v[3][i] = p.mfma ? v[2][i] : expert_units(n);          // MFMA tiles are one unit each
+        // MFMA tiles by size: full tiles and a remainder of more than 16 rows are large
+        const int rest = n & ((1 << cs) - 1);
+        v[4][i] = p.mfma && rest > 0 && rest <= 16 ? 1 : 0;
+        v[5][i] = p.mfma ? (n >> cs) + (rest > 16 ? 1 : 0) : 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) tot[k] += v[k][i];
+        for (int k = 0; k < 6; ++k) tot[k] += v[k][i];
     }
-    int run[4];
+    int run[6];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) run[k] = wave_incl_scan(tot[k]);
-    int* const dst[4] = {ex.off, ex.run_base, ex.chunk_base, ex.unit_base};
+    for (int k = 0; k < 6; ++k) run[k] = wave_incl_scan(tot[k]);
+    int* const dst[6] = {ex.off, ex.run_base, ex.chunk_base, ex.unit_base, ex.small_base, ex.large_base};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 6; ++k) {
         int r = run[k] - tot[k];
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
@@ -493,6 +500,15 @@ __device__ void group_slots_par(const MoeParams& p, const SelT* sel, const half_
 // Chunks of <= chunk_rows_of(p) slots per expert, then the shared expert's rows; for the decode
 // GEMV also their work units (unit -> chunk map) and each slot's chunk weight. `order` is the
 // grouped slot order.
+// MFMA mode: files tile ci under its size class, in chunk (expert) order within each class: the
+// tiles of at most 16 rows from the front of p.tiles, the larger ones from the back. si / li
+// are the tile's index within its class.
+__device__ __forceinline__ void file_tile(const MoeParams& p, int ci, int rows, int si, int li)
+{
+    if (rows <= 16) p.tiles[si] = ci;
+    else p.tiles[p.max_chunks - 1 - li] = ci;
+}
+
 __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int* order)
 {
     const int t = threadIdx.x, nt = blockDim.x;
@@ -519,6 +535,8 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
             if (!p.mfma)                 // MFMA tiles weigh 1: filled in parallel below
                 for (int i = 0; i < rows; ++i) p.slot_mult[order[c[1] + i]] = m;
+            else
+                file_tile(p, ci, rows, ex.small_base[e], ex.large_base[e] + j);   // a small tile is the last
             u += m;
         }
     }
@@ -542,10 +560,17 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
             if (!p.mfma)
                 for (int i = 0; i < rows; ++i) p.slot_mult[slots + j * CR + i] = m;
+            else                         // shared tiles follow the routed ones; only the last can be small
+                file_tile(p, base + j, rows, ex.small_base[E], ex.large_base[E] + j);
         }
     }
-    if (p.mfma)
+    if (p.mfma) {
         for (int s = t; s < moe_nslot(p); s += nt) p.slot_mult[s] = 1;
+        if (t == 0) {
+            const int sh_rest = p.has_shared ? p.T % CR : 0;
+            p.meta[3] = ex.small_base[E] + (sh_rest > 0 && sh_rest <= 16 ? 1 : 0);
+        }
+    }
 }
 
 __device__ __forceinline__ int total_chunks(const MoeParams& p, const ExpertLds& ex)

@@ -201,26 +201,38 @@ __device__ __forceinline__ int xcd_item_block(int b, int nb)
 // which = 1: down, items (tile, cg, ks) with cg over H/128 -> part_d[ks][slot][H].
 // Every tile is one work unit of weight 1; the k-split is the decode GEMV's (moe_ksplit: as many
 // splits as fill the resident grid once, or the requested count), so the activation and combine
-// kernels sum the same partials. MBMAX bounds the tile rows in 16-row blocks (1: at most 16 rows,
-// i.e. calls of at most 16 tokens, with a quarter of the accumulators).
+// kernels sum the same partials. MBMAX bounds the tile rows in 16-row blocks: the MBMAX 1 kernel
+// (a quarter of the accumulators, 3 waves per SIMD) runs the tiles of at most 16 rows, the
+// MBMAX 4 kernel the larger ones; the split count is the same for both (from all the tiles).
 template <int MBMAX>
 __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(MBMAX == 1 ? 3 : 2))) void moe_mfma_kernel(MoeParams p, int which)
 {
     __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
     const int wave = threadIdx.x >> 6;
-    const int n_tiles = __builtin_amdgcn_readfirstlane(p.meta[0]);
+    const int n_all = __builtin_amdgcn_readfirstlane(p.meta[0]);
+    const int n_small = __builtin_amdgcn_readfirstlane(p.meta[3]);
     const int ncg = which == 0 ? p.I / 128 : p.H / 128;
-    const KSplit k = which == 0 ? ks_gate_up(p, n_tiles) : ks_down(p, n_tiles);
+    const KSplit k = which == 0 ? ks_gate_up(p, n_all) : ks_down(p, n_all);
     const int S = ks_of_chunk(k, 1);
     const int per_tile = (which == 0 ? 2 * ncg : ncg) * S;
+    // this launch's tiles: the small ones (at most 16 rows) in the MBMAX 1 kernel when they fill
+    // at least three of its resident rounds (3 waves per SIMD), so that its last round's tail is
+    // short; the rest (or all) in the MBMAX 4 kernel. Up to 16 tokens every tile is small.
+    const bool split = p.T <= 16 || (long)n_small * per_tile >= 3L * (p.gemv_waves * 3 / 4);
+    const int n_tiles = MBMAX == 1 ? (split ? n_small : 0) : (split ? n_all - n_small : n_all);
     // the call's items fill the first n_blk workgroups (a multiple of 8, spread over the XCDs)
     const int n_blk = ((n_tiles * per_tile + MF_WAVES - 1) / MF_WAVES + 7) & ~7;
     if ((int)blockIdx.x >= n_blk) return;
     const int blk = xcd_item_block(blockIdx.x, n_blk);
     const int item = __builtin_amdgcn_readfirstlane(blk * MF_WAVES + wave);
-    const int tile = item / per_tile;
-    if (tile >= n_tiles) return;
-    const int rem = item - tile * per_tile;
+    const int ti = item / per_tile;
+    if (ti >= n_tiles) return;
+    // split: the small tiles from the front of the list, the large ones from the back, each in
+    // expert order; otherwise all tiles in chunk order (the tiles of one expert run side by side
+    // and share its weight reads in L2)
+    const int tile = __builtin_amdgcn_readfirstlane(
+        !split ? ti : MBMAX == 1 ? p.tiles[ti] : p.tiles[p.max_chunks - 1 - ti]);
+    const int rem = item - ti * per_tile;
     const int ks = rem % S;
     const int pc = rem / S;
     const int proj = which == 0 ? pc / ncg : 2;
@@ -288,10 +300,14 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     (void)kmax;
     long blocks = (items + MF_WAVES - 1) / MF_WAVES;
     blocks = (blocks + 7) & ~7L;
-    if (p.T <= 16)
+    // tiles of at most 16 rows run in the 16-row kernel (3 waves per SIMD, progress priorities),
+    // larger ones in the 64-row kernel; up to 16 tokens every tile is a small one
+    if (p.T <= 16) {
         launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
-    else
-        launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
+    } else {
+        launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, nullptr, p, which);
+        launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, nullptr, stop, p, which);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
