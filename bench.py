@@ -177,10 +177,11 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=("layer", "stack", "prefill"), default="layer",
+    ap.add_argument("--workload", choices=("layer", "stack", "prefill", "linear"), default="layer",
                     help="layer: one decode layer (configs[1] at 1 token, configs[2] at 16); stack: configs[4], "
                          "58 stacked layers at 2.5 bpw, 8 tokens, one hipGraph; prefill: configs[3], 512 tokens, "
-                         "Zipf routing, per-expert rates {2,3,4,5}")
+                         "Zipf routing, per-expert rates {2,3,4,5}; linear: configs[0], one EXL3 linear "
+                         "2048 -> 7168 at 4 bpw, 1 token, over 64 resident copies in one graph")
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--bits", type=float, default=None)
     ap.add_argument("--layers", type=int, default=None)
@@ -194,7 +195,7 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
-    defaults = {"layer": (1, 4.0, 4), "stack": (8, 2.5, 58), "prefill": (512, None, 2)}[args.workload]
+    defaults = {"layer": (1, 4.0, 4), "stack": (8, 2.5, 58), "prefill": (512, None, 2), "linear": (1, 4.0, 64)}[args.workload]
     if args.tokens is None:
         args.tokens = defaults[0]
     if args.bits is None:
@@ -218,6 +219,8 @@ def main():
         return
     if args.workload == "stack":
         result = run_stack(torch, args)
+    elif args.workload == "linear":
+        result = run_linear(torch, args)
     else:
         result = run_layer(torch, args)
     print(json.dumps(result), flush=True)
@@ -463,6 +466,98 @@ def run_stack(torch, args):
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(bits=K, tokens=T, n_routed=1)
     return result
+
+
+def run_linear(torch, args):
+    """one EXL3 linear 2048 -> 7168 at 4 bpw on 1 token. A call moves 7.4 MB, so it is
+    launch-bound: `--layers` resident copies (default 64) are cycled in one graph, and the time per
+    call is the graph's time over the calls."""
+    from eva_amd import ops
+
+    dev = torch.device("cuda", 0)
+    n_in, n_out, T, copies = 2048, 7168, args.tokens, args.layers
+    bits = args.bits
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    tu = tile_u16(bits)
+    trellis = torch.randint(-32768, 32768, (copies, n_in // 16, n_out // 16, tu), generator=g, device=dev,
+                            dtype=torch.int32).to(torch.int16)
+    suh = (torch.randint(0, 2, (copies, n_in), generator=g, device=dev) * 2 - 1).to(torch.float16)
+    mag = torch.rand((copies, n_out), generator=g, device=dev) + 0.5
+    svh = ((torch.randint(0, 2, (copies, n_out), generator=g, device=dev) * 2 - 1) * mag).to(torch.float16)
+    x = torch.randn((T, n_in), generator=g, device=dev).to(torch.bfloat16).to(torch.float16)
+    out = torch.empty(copies, T, n_out, dtype=torch.float16, device=dev)
+    ws = torch.empty(ops.lib().evamx_exl3_linear_workspace_bytes(T, n_in, n_out), dtype=torch.uint8, device=dev)
+
+    def call(i):
+        ops.exl3_linear(x, trellis[i], suh[i], svh[i], bits, out=out[i], workspace=ws)
+
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for i in range(copies):
+            call(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(copies):
+                call(i)
+    eager = out.clone()
+    reps = max(1, args.steps // copies)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup // copies)):
+            graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            graph.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / (reps * copies)
+    if not torch.equal(out, eager):
+        raise RuntimeError("graph replays differ from the eager calls")
+    nbytes = n_in * n_out * bits / 8 + 2 * (n_in + n_out) + T * 2 * (n_in + n_out)
+    gbps = nbytes / dt / 1e9
+    result = {
+        "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": reps * copies, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 6),
+        "us_per_call": round(dt * 1e6, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5) svh, bf16 N(0,1) x)",
+        "config": {"workload": f"single EXL3 linear {n_in} -> {n_out}, {bits:g} bpw, {T} token(s), "
+                               f"{copies} resident copies in one graph (BASELINE configs[0])",
+                   "in": n_in, "out": n_out, "tokens": T, "bits": bits, "copies": copies},
+        "step_bytes": int(nbytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
+        "roofline": {"bound": "hbm", "kernel": "exl3_linear (3 launches per call)", "achieved": round(gbps, 1),
+                     "peak": PEAK_HBM, "unit": "GB/s", "frac": round(gbps / PEAK_HBM, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_linear_baseline(torch, n_in, n_out, bits, T)
+    return result
+
+
+def cpu_linear_baseline(torch, n_in, n_out, bits, T, min_seconds=10.0):
+    """The PyTorch-CPU restatement of the same linear (LUT decode, H128 matmuls, fp32 product)."""
+    import numpy as np
+
+    from oracle import synth, torch_cpu
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(5)
+    tr, suh, svh = (torch.from_numpy(np.ascontiguousarray(a)) for a in synth.projection(rng, n_in, n_out, bits))
+    dec = torch_cpu.Decoder(bits)
+    x = torch.from_numpy(synth.activations_bf16(rng, T, n_in))
+    torch_cpu.linear_forward(x, tr, suh, svh, dec)
+    times = []
+    while len(times) < 2 or (sum(times) < min_seconds and len(times) < 50):
+        t0 = time.perf_counter()
+        torch_cpu.linear_forward(x, tr, suh, svh, dec)
+        times.append(time.perf_counter() - t0)
+    t = sum(times) / len(times)
+    nbytes = n_in * n_out * bits / 8 + 2 * (n_in + n_out)
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"the same {n_in} -> {n_out} linear at {bits:g} bpw, {T} token(s) (mean of {len(times)} runs "
+                      f"after 1 warm-up; {t * 1e3:.1f} ms each)",
+            "seconds_per_sample": round(t, 4), "torch_threads": torch.get_num_threads()}
 
 
 def gate_up_roofline(bytes_launch, us, traffic):

@@ -68,6 +68,12 @@ class Decoder:
         return tiles.permute(0, 2, 1, 3).reshape(kt * 16, nt * 16)
 
 
+def linear_forward(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                   dec: Decoder) -> torch.Tensor:
+    """One EXL3 linear (ELinear.forward, exl3_linear.py:97-131), fp32: H(H(x*suh) @ W) * svh."""
+    return rotate(rotate(x * suh.float()) @ dec.dequant(trellis)) * svh.float()
+
+
 def expert_forward(x: torch.Tensor, parts, dec: Decoder, limit: float, shared: bool) -> torch.Tensor:
     """x fp32 [R, H]; parts = ((trellis, suh, svh) for g, u, d) as CPU tensors."""
     outs = []
