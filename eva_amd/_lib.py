@@ -54,6 +54,8 @@ _SIGNATURES = {
     "evamx_exl3_linear_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "evamx_exl3_linear": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp, _f32,
                                          _vp, _vp, ctypes.c_size_t, _vp]),
+    "evamx_router_logits": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int,
+                                           ctypes.c_int, _vp, _vp]),
     "evamx_route_topk": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32,
                                         _vp, _vp, _vp, _vp]),
     "evamx_prepare_routes_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),

@@ -217,6 +217,27 @@ extern "C" int evamx_route_topk(const float* logits, const float* sel_bias, int 
     return launched("route_topk");
 }
 
+extern "C" int evamx_router_logits(const void* x, int x_dtype, int x_stride, int rows, const float* gate_w,
+                                   int n_experts, int hidden, float* logits, evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    EVAMX_REQUIRE(x && gate_w && logits, "evamx_router_logits: null pointer");
+    EVAMX_REQUIRE(x_dtype == EVAMX_DTYPE_F16 || x_dtype == EVAMX_DTYPE_BF16, "evamx_router_logits: x_dtype %d", x_dtype);
+    EVAMX_REQUIRE(rows >= 1 && rows <= 65536, "evamx_router_logits: rows %d outside 1..65536", rows);
+    EVAMX_REQUIRE(n_experts >= 1 && n_experts <= EVAMX_MAX_EXPERTS, "evamx_router_logits: n_experts %d outside 1..%d",
+                  n_experts, EVAMX_MAX_EXPERTS);
+    EVAMX_REQUIRE(hidden >= 4 && hidden % 4 == 0 && x_stride >= hidden,
+                  "evamx_router_logits: hidden %d must be a positive multiple of 4 and x_stride >= hidden", hidden);
+    EVAMX_REQUIRE(((uintptr_t)gate_w & 15) == 0, "evamx_router_logits: gate_w must be 16-byte aligned");
+    MoeParams p;
+    memset(&p, 0, sizeof p);
+    p.T = rows; p.H = hidden; p.n_logits = n_experts;
+    p.x = x; p.x_dtype = x_dtype; p.x_stride = x_stride;
+    p.gate_w = gate_w;
+    launch_router_logits(p, logits, (hipStream_t)stream);
+    return launched("router_logits");
+}
+
 extern "C" size_t evamx_prepare_routes_workspace_bytes(int capacity, int topk)
 {
     if (capacity < 1 || topk < 1) return 0;

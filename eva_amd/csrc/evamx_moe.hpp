@@ -150,6 +150,7 @@ inline void launch_timed(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStr
 
 int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 int moe_prepare_only(MoeParams& p, hipStream_t stream);
+int launch_router_logits(const MoeParams& p, float* logits, hipStream_t stream);
 bool moe_small_path(int T, int topk);
 
 }  // namespace evamx

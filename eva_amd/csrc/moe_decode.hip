@@ -1160,6 +1160,13 @@ int moe_prepare_only(MoeParams& p, hipStream_t stream)
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+int launch_router_logits(const MoeParams& p, float* logits, hipStream_t stream)
+{
+    const int waves = p.n_logits * ((p.T + GATE_ROWS - 1) / GATE_ROWS);
+    hipLaunchKernelGGL(moe_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p, logits);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T <= EVAMX_SMALL_ROWS; }
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)

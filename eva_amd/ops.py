@@ -88,6 +88,40 @@ def route_topk(logits: torch.Tensor, topk: int, score_fn: str = "sigmoid", sel_b
     return idx, w, rw
 
 
+def router_logits(x: torch.Tensor, gate_w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 ``x.float() @ gate_w.T`` on the device (``evamx_router_logits``), each row reduced in one
+    fixed order whatever the batch (model.py:158-165)."""
+    if x.dim() != 2 or x.dtype not in (torch.float16, torch.bfloat16) or not x.is_cuda or x.stride(1) != 1:
+        raise ValueError("x must be a CUDA fp16/bf16 [rows, hidden] tensor with unit inner stride")
+    _dev(gate_w, "gate_w", torch.float32, 2)
+    rows, hidden = x.shape
+    if gate_w.shape[1] != hidden:
+        raise ValueError(f"gate_w must be [n_experts, {hidden}]")
+    if out is None:
+        out = torch.empty(rows, gate_w.shape[0], dtype=torch.float32, device=x.device)
+    _dev(out, "out", torch.float32, 2)
+    check(lib().evamx_router_logits(ptr(x), _lib.DTYPE_BF16 if x.dtype == torch.bfloat16 else _lib.DTYPE_F16, x.stride(0), rows,
+                                    ptr(gate_w), gate_w.shape[0], hidden, ptr(out), stream_handle(x.device)),
+          "evamx_router_logits")
+    return out
+
+
+def route(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor | None, topk: int, route_scale: float = 1.0,
+          score_fn: str = "sqrt_softplus", image_mask: torch.Tensor | None = None,
+          gate_b_vl: torch.Tensor | None = None):
+    """``Block.route(x, image_mask) -> (w, idx)`` (model.py:404-416) on the device: gate GEMV, scores,
+    top-k of score + bias (``gate_b_vl`` for the rows of ``image_mask``), weights normalised and
+    scaled. With a mask both biases are routed and the rows picked by ``torch.where`` (no host sync)."""
+    z = router_logits(x, gate_w)
+    idx, w, _ = route_topk(z, topk, score_fn, gate_b, route_scale)
+    if image_mask is not None and gate_b_vl is not None:
+        idx_vl, w_vl, _ = route_topk(z, topk, score_fn, gate_b_vl, route_scale)
+        m = image_mask.reshape(-1, 1).to(device=z.device, dtype=torch.bool)
+        idx = torch.where(m, idx_vl, idx)
+        w = torch.where(m, w_vl, w)
+    return w, idx
+
+
 def prepare_routes_workspace_bytes(capacity: int, topk: int) -> int:
     n = lib().evamx_prepare_routes_workspace_bytes(capacity, topk)
     if n == 0:

@@ -11,6 +11,8 @@
  *                            codebook.cuh:86-99 (the "decoded fp16 weight" contract)
  *   evamx_exl3_linear        ELinear.forward -> LinearEXL3 (exl3_linear.py:97-131,134-154),
  *                            kernel csrc/moe_coop3072/vendor/quant/exl3_gemv_kernel.cuh:195-491
+ *   evamx_router_logits      the gate GEMV of Block.route, stable_linear(x.float(), gate_w)
+ *                            (model.py:158-165,404-409; stable_linear_runtime "router" dispatch)
  *   evamx_route_topk         Block.route (model.py:404-416) with the stable tie rule of
  *                            _stable_topk_indices (model.py:940-953)
  *   evamx_prepare_routes     CoopRunner3072.prepare_routes -> pybind prepare_routes
@@ -65,6 +67,13 @@ int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, int out_fea
                       void* y_fp16, void* workspace, size_t workspace_bytes, evamx_stream_t stream);
 
 /* ---- router ------------------------------------------------------------------------------ */
+
+/* logits[r][e] = sum_k float(x[r][k]) * gate_w[e][k] (fp32): the router gate GEMV of
+ * Block.route, stable_linear(x.float(), gate_w) (model.py:158-165,404-409). Each row's sums run
+ * in one fixed order whatever `rows` is (batch invariant). x: device fp16/bf16 [rows][x_stride];
+ * gate_w: device fp32 [n_experts][hidden], 16-byte aligned; hidden a multiple of 4. */
+int evamx_router_logits(const void* x, int x_dtype, int x_stride, int rows, const float* gate_w,
+                        int n_experts, int hidden, float* logits, evamx_stream_t stream);
 
 /* indices[r][j], weights[r][j] (fp32) and rw_fp16[r][j] = fp16(weights) for the top `topk`
  * experts of each row of logits [rows][n_experts]: selection key score(z) + sel_bias (or z

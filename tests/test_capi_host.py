@@ -132,6 +132,12 @@ def test_other_entry_points_reject_bad_arguments():
     assert L.evamx_bench_decode(4.0, 4094, 10, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_bench_decode(4.0, 4096, 0, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_bench_decode(4.0, 4096, 10, None, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7168, 1, FAKE, 256, 7168, None, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_router_logits(FAKE, 5, 7168, 1, FAKE, 256, 7168, FAKE, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7168, 1, FAKE, 600, 7168, FAKE, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7100, 1, FAKE, 256, 7168, FAKE, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7168, 1, FAKE + 8, 256, 7168, FAKE, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7168, 0, FAKE, 256, 7168, FAKE, None) == _lib.EVAMX_EINVAL
 
 
 def test_product_path_does_not_import_the_oracle():

@@ -140,3 +140,39 @@ def test_gate_weight_path_is_graph_capturable(dev):
         fwd()
         torch.cuda.synchronize()
         assert torch.equal(idx_graph, sel) and torch.equal(w_graph, w) and torch.equal(y_graph, out), rep
+
+
+@pytest.mark.parametrize("rows", [1, 7, 33])
+def test_block_route_mirror(dev, rows):
+    """ops.route (Block.route, model.py:404-416): standalone logits within the bound and equal to the
+    fused forward's; sqrt-softplus scores with gate_b, gate_b_vl on the image rows, route_scale 2.5;
+    indices and weights bit-exact against the oracle router on those logits."""
+    ops = _ops()
+    H, E, topk = 7168, 256, 8
+    rng = np.random.default_rng(100 + rows)
+    x = synth.activations_bf16(rng, rows, H)
+    gate_w = _gate(rng, E, H)
+    gate_b = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    gate_b_vl = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    mask = rng.integers(0, 2, size=rows).astype(bool)
+    xt = to_dev(x, dev).to(torch.bfloat16)
+    z = ops.router_logits(xt, to_dev(gate_w, dev))
+    w, idx = ops.route(xt, to_dev(gate_w, dev), to_dev(gate_b, dev), topk, route_scale=2.5,
+                       image_mask=torch.from_numpy(mask).to(dev), gate_b_vl=to_dev(gate_b_vl, dev))
+    torch.cuda.synchronize()
+    zn = z.cpu().numpy().copy()
+    _check_logits(zn, xt.float().cpu().numpy(), gate_w)
+    for r in range(rows):
+        ridx, rw = coop.route(zn[r:r + 1], topk, "sqrt_softplus", gate_b_vl if mask[r] else gate_b, 2.5)
+        assert np.array_equal(idx[r].cpu().numpy(), ridx[0]), r
+        assert np.array_equal(w[r].cpu().numpy(), rw[0]), r
+    # the standalone gate GEMV and the fused one are the same kernel: bit-identical logits
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=2048, topk=topk, n_local=E, has_shared=False)
+    dummy = DeviceExperts([synth.expert(rng, H, 2048, 2, 1 / np.sqrt(H))], dev)
+    sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
+    wt = torch.empty(rows, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, xt, dummy.table[:, :1].expand(9, E).contiguous(), out, limit=10.0, bits=2,
+                    gate_w=to_dev(gate_w, dev), sel=sel, weights=wt)
+    torch.cuda.synchronize()
+    assert np.array_equal(ws.logits(rows, E).cpu().numpy().view(np.uint32), zn.view(np.uint32))
