@@ -297,13 +297,21 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     const long auto_items = (long)p.gemv_waves + per_tile;   // an automatic split fills one resident round
     const long items = kreq > 0 ? (long)p.max_chunks * per_tile * kreq
                                 : (p.max_chunks * per_tile > auto_items ? (long)p.max_chunks * per_tile : auto_items);
-    (void)kmax;
     long blocks = (items + MF_WAVES - 1) / MF_WAVES;
     blocks = (blocks + 7) & ~7L;
     // tiles of at most 16 rows run in the 16-row kernel (3 waves per SIMD, progress priorities),
     // larger ones in the 64-row kernel; up to 16 tokens every tile is a small one
+    // The small-tile launch is skipped when the split can never happen: at most one tile per
+    // expert (its remainder) and one shared tile are small, at the largest split count
+    const int nslot = p.T * p.topk + (p.has_shared ? p.T : 0);
+    const int cap_rows = which == 0 ? p.cap_rows_gu : p.cap_rows_d;
+    const int s_max = kreq > 0 ? kreq : (cap_rows / nslot < kmax ? (cap_rows / nslot > 1 ? cap_rows / nslot : 1) : kmax);
+    const long max_small = (long)(p.n_local < p.T * p.topk ? p.n_local : p.T * p.topk) + (p.has_shared ? 1 : 0);
+    const bool may_split = max_small * per_tile * s_max >= 3L * (p.gemv_waves * 3 / 4);
     if (p.T <= 16) {
         launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
+    } else if (!may_split) {
+        launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
     } else {
         launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, nullptr, p, which);
         launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, nullptr, stop, p, which);
