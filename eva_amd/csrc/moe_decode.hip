@@ -4,20 +4,23 @@
 // (runtime/ds41/csrc/moe_coop3072/moe_coop3072.cu:42-71). Cross-workgroup results only ever
 // cross a kernel boundary: a device-scope release fence costs an L2 write-back on this
 // multi-XCD part, far more than a launch when thousands of waves would each need one. Five
-// launches on one stream, no host synchronisation, no memset (graph-capturable):
+// stages on one stream, no host synchronisation, no memset (graph-capturable):
 //
+//   (gate)        optional router front: fp32 logits x . gate_w (model.py:404-409)
 //   moe_prepare   routing (optional), slot activity + bounds flag, stable grouping by expert
 //                 (the reference run table, runs <= 8 slots: prepare_runs.cuh:8-66; and chunks
-//                 of <= 16 slots for the GEMV work items), then the input rotation
-//                 fp16(H128(x * suh)) of every active slot (exl3_moe_coop_kernel.cuh:613-629;
-//                 shared expert: fp16 pre-scale, hadamard_inner.cuh:109-115). For <= 16 rows
-//                 every workgroup groups redundantly in LDS and rotates its share; workgroup 0
-//                 publishes the tables.
+//                 of <= 8 slots for the GEMV work items, or tiles of <= 64 for the MFMA path),
+//                 then the input rotation fp16(H128(x * suh)) of every active slot
+//                 (exl3_moe_coop_kernel.cuh:613-629; shared expert: fp16 pre-scale,
+//                 hadamard_inner.cuh:109-115). For <= 16 rows one kernel: every workgroup
+//                 routes, workgroup 0 groups and publishes the tables, the others rotate.
 //   moe_gate_up   per (chunk, gate|up, 128 columns, k-split) wave: decode GEMV -> fp32 partials
+//                 (8 rows and more: MFMA tiles, moe_prefill.hip)
 //   moe_act       per (active slot, 128 columns of I): sums the gate/up partials in fixed
 //                 order, rounds to fp16 (gu_f32 = false), and runs the activation epilogue
 //                 (exl3_moe_coop_kernel.cuh:758-806; shared expert: model.py:450-452)
 //   moe_down      per (chunk, 128 columns, k-split) wave: decode GEMV -> fp32 partials
+//                 (8 rows and more: MFMA tiles)
 //   moe_combine   per (token, 128 columns): output rotation * svh * routing weight, summed over
 //                 the token's slots in slot order, plus the shared expert
 //                 (exl3_moe_coop_kernel.cuh:860-962, model.py:498)
