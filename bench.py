@@ -191,6 +191,9 @@ def parse_args():
     ap.add_argument("--routing", choices=("plain", "skewed"), default=None,
                     help="N(0,1) logits, or config 3's per-token bias (default: plain at 1 token, skewed above)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--also-tokens", type=int, default=16,
+                    help="with the default 1-token layer, also measure this many tokens (configs[2]) and report "
+                         "it under \"also\" in the same line (0: off)")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE)")
@@ -223,6 +226,19 @@ def main():
         result = run_linear(torch, args)
     else:
         result = run_layer(torch, args)
+        if args.workload == "layer" and args.tokens == 1 and args.also_tokens > 0:
+            # the metric covers 1 and 16 tokens: the second point rides along in the same line
+            import copy
+            import gc
+
+            gc.collect()
+            torch.cuda.empty_cache()
+            sub = copy.copy(args)
+            sub.tokens, sub.routing, sub.no_cpu_baseline = args.also_tokens, None, True
+            r2 = run_layer(torch, sub)
+            result["also"] = {k: r2[k] for k in ("us_per_layer", "value", "unit", "step_bytes", "frac_hbm_step",
+                                                 "kernel_us", "roofline")}
+            result["also"]["config"] = r2["config"]["workload"]
     print(json.dumps(result), flush=True)
 
 
