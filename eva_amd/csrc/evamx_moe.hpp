@@ -123,14 +123,24 @@ __device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
     return v < k.cap ? v : k.cap;
 }
 
+// Waves the automatic split aims for: one resident round (4 per SIMD), except for one-row calls,
+// whose GEMV waves aim for two per SIMD. With progress priorities two one-row waves keep a SIMD's
+// VALU as busy as four, and half the waves halve the prologues and the partials the next stage
+// sums (T=1 82.4 -> 79.6 us); with more rows per chunk two waves per SIMD lose (T=2 116 -> 122,
+// T=4 174 -> 255 us).
+__device__ __forceinline__ int split_waves(const MoeParams& p)
+{
+    return (!p.mfma && p.T == 1) ? p.gemv_waves / 2 : p.gemv_waves;
+}
+
 __device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
 {
-    return moe_ksplit(p.ks_gu, units * 2 * (p.I / 128), p.gemv_waves, p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
+    return moe_ksplit(p.ks_gu, units * 2 * (p.I / 128), split_waves(p), p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
 }
 
 __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
 {
-    return moe_ksplit(p.ks_d, units * (p.H / 128), p.gemv_waves, p.ks_d_max, p.cap_rows_d, moe_nslot(p));
+    return moe_ksplit(p.ks_d, units * (p.H / 128), split_waves(p), p.ks_d_max, p.cap_rows_d, moe_nslot(p));
 }
 
 __host__ __device__ __forceinline__ int chunk_rows_of(const MoeParams& p) { return p.chunk_rows > 0 ? p.chunk_rows : EVAMX_CHUNK; }
