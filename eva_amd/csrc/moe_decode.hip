@@ -15,12 +15,12 @@
 //                 hadamard_inner.cuh:109-115). For <= 16 rows one kernel: every workgroup
 //                 routes, workgroup 0 groups and publishes the tables, the others rotate.
 //   moe_gate_up   per (chunk, gate|up, 128 columns, k-split) wave: decode GEMV -> fp32 partials
-//                 (8 rows and more: MFMA tiles, moe_prefill.hip)
+//                 (3 rows and more: MFMA tiles, moe_prefill.hip)
 //   moe_act       per (active slot, 128 columns of I): sums the gate/up partials in fixed
 //                 order, rounds to fp16 (gu_f32 = false), and runs the activation epilogue
 //                 (exl3_moe_coop_kernel.cuh:758-806; shared expert: model.py:450-452)
 //   moe_down      per (chunk, 128 columns, k-split) wave: decode GEMV -> fp32 partials
-//                 (8 rows and more: MFMA tiles)
+//                 (3 rows and more: MFMA tiles)
 //   moe_combine   per (token, 128 columns): output rotation * svh * routing weight, summed over
 //                 the token's slots in slot order, plus the shared expert
 //                 (exl3_moe_coop_kernel.cuh:860-962, model.py:498)
