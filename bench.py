@@ -371,6 +371,8 @@ def run_layer(torch, args):
                             "flops_per_launch": flops}
     else:
         roofline["decode_alu_ceiling"] = decode_ceiling(ops, (args.bits,), roofline["achieved"])
+        if T == 1 and args.bits == 4.0:
+            roofline["read_floor"] = read_floor(torch, ops, H, I, TOPK + 1, roofline["achieved"])
     cfg_idx = 3 if prefill else (1 if T == 1 else 2)
     rates = "per-expert rates {2,3,4,5} (shared 4)" if prefill else f"{args.bits:g} bpw"
     result = {
@@ -596,6 +598,25 @@ def decode_ceiling(ops, bits_list, achieved_gbps=None, weights=None):
     if achieved_gbps is not None and len(per) == 1:
         out["frac"] = round(achieved_gbps / out["value"], 4)
     return out
+
+
+def read_floor(torch, ops, H, I, units, achieved_gbps):
+    """Memory-side bound of the one-row gate/up launch (evamx_bench_read): the launch's own bytes
+    in its own shape, without the decode. One-row calls aim their k-split at two waves per SIMD:
+    units x (gate, up) x I/128 column groups x ks waves, ks = that target over the per-split
+    items, each wave streaming the 8 * (H/128 / ks) k-slices of its split as 1 KiB chunks (8 tiles
+    at 4 bits), four in flight. Back-to-back launches, so the figure includes each launch's ramp
+    and tail but only part of the gap between launches."""
+    ncg = I // 128
+    per_split = units * 2 * ncg
+    waves_target = torch.cuda.get_device_properties(0).multi_processor_count * 16 // 2
+    ks = max(1, waves_target // per_split)
+    rows = 8 * ((H // 128) // ks)
+    waves = per_split * ks
+    bps = ops.read_floor(ncg, rows, waves)
+    return {"kernel": "evamx_bench_read", "unit": "GB/s", "value": round(bps / 1e9, 1),
+            "bytes_per_launch": waves * rows * 1024, "waves": waves, "slices_per_wave": rows,
+            "frac": round(achieved_gbps / (bps / 1e9), 4)}
 
 
 COPY_BYTES = 1 << 30

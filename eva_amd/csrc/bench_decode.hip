@@ -5,6 +5,10 @@
 // instruction mix of the decode GEMV's inner loop for one row. Bench.py divides the trellis
 // bytes this rate implies into a GEMV's achieved bytes to say how close the GEMV is to the
 // arithmetic bound, as opposed to the HBM bound.
+//
+// Read floor: the bytes of a decode GEMV launch streamed in that launch's shape without the
+// decode, for the memory-side bound of the same launch (the HBM peak is reached only by long
+// streams; a launch of tens of microseconds also pays its ramp and tail).
 #include "evamx_gemv.hpp"
 #include "evamx_internal.hpp"
 
@@ -33,6 +37,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void b
     }
     // keep the work observable without storing per lane
     if (a0 + a1 == 1234.5f) sink[threadIdx.x] = a0;
+}
+
+// Wave w = (chain, cg), cg = w % ncg: the wave's 64 lanes read 16 bytes each from row
+// chain * rows + i, at byte cg * 1024 of the row, for i < rows, with four rows in flight (the
+// GEMV's prefetch depth and its non-temporal 16-byte loads); rows are row_u4 * 16 bytes apart.
+__global__ __launch_bounds__(256) void bench_read_kernel(const u32x4* __restrict__ base, int ncg, int rows, int row_u4,
+                                                         int n_waves, float* sink)
+{
+    const int w = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    if (w >= n_waves) return;
+    const int lane = threadIdx.x & 63;
+    const int cg = w % ncg, chain = w / ncg;
+    const u32x4* q = base + (size_t)chain * rows * row_u4 + (size_t)cg * 64 + lane;
+    uint32_t acc = 0;
+    for (int i = 0; i < rows; i += 4) {
+        u32x4 v[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            v[d] = i + d < rows ? __builtin_nontemporal_load(q + (size_t)(i + d) * row_u4) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+    }
+    // keep the loads observable without storing per lane
+    if (acc == 0x12345678u) sink[lane] = 1.0f;
+}
+
+void launch_bench_read(const void* base, int ncg, int rows, int n_waves, float* sink, hipStream_t stream)
+{
+    hipLaunchKernelGGL(bench_read_kernel, dim3((unsigned)((n_waves + 3) / 4)), dim3(256), 0, stream, (const u32x4*)base,
+                       ncg, rows, ncg * 64, n_waves, sink);
 }
 
 int launch_bench_decode(int k2, int blocks, int iters, float* sink, hipStream_t stream)

@@ -421,3 +421,18 @@ extern "C" int evamx_bench_decode(float bits, int waves, int iters, float* sink,
     launch_bench_decode(k2, waves / 4, iters, sink, (hipStream_t)stream);
     return launched("bench_decode");
 }
+
+extern "C" int evamx_bench_read(const void* buf, size_t bytes, int ncg, int rows, int waves, float* sink,
+                                evamx_stream_t stream)
+{
+    g_err[0] = 0;
+    EVAMX_REQUIRE(buf && sink, "evamx_bench_read: null buffer or sink");
+    EVAMX_REQUIRE(ncg >= 1 && ncg <= 4096, "evamx_bench_read: ncg %d outside 1..4096", ncg);
+    EVAMX_REQUIRE(rows >= 1 && rows <= (1 << 20), "evamx_bench_read: rows %d outside 1..%d", rows, 1 << 20);
+    EVAMX_REQUIRE(waves >= ncg && waves <= (1 << 22) && waves % ncg == 0,
+                  "evamx_bench_read: waves %d not a multiple of ncg %d in %d..%d", waves, ncg, ncg, 1 << 22);
+    const double need = (double)(waves / ncg) * rows * ncg * 1024.0;
+    EVAMX_REQUIRE(need <= (double)bytes, "evamx_bench_read: the shape reads %.0f bytes, the buffer holds %zu", need, bytes);
+    launch_bench_read(buf, ncg, rows, waves, sink, (hipStream_t)stream);
+    return launched("bench_read");
+}

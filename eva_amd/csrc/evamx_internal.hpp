@@ -22,5 +22,6 @@ int launch_linear(const void* x, int rows, int in, int out, const void* trellis,
 namespace evamx {
 
 int launch_bench_decode(int k2, int blocks, int iters, float* sink, hipStream_t stream);
+void launch_bench_read(const void* base, int ncg, int rows, int n_waves, float* sink, hipStream_t stream);
 
 }  // namespace evamx

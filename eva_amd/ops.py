@@ -271,6 +271,26 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     return out
 
 
+def read_floor(ncg: int, rows: int, waves: int, device=None, reps: int = 50) -> float:
+    """Bytes per second of the read-only benchmark (evamx_bench_read): ``waves`` waves stream
+    ``rows`` 1 KiB chunks each in a decode GEMV launch's shape (wave w reads column group w % ncg
+    of its chain's rows), no decode; ``reps`` back-to-back launches timed with events."""
+    dev = torch.device("cuda", 0) if device is None else torch.device(device)
+    nbytes = (waves // ncg) * rows * ncg * 1024
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(64, dtype=torch.float32, device=dev)
+    stream = stream_handle(dev)
+    check(lib().evamx_bench_read(ptr(buf), nbytes, ncg, rows, waves, ptr(sink), stream), "evamx_bench_read")   # warm-up
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        check(lib().evamx_bench_read(ptr(buf), nbytes, ncg, rows, waves, ptr(sink), stream), "evamx_bench_read")
+    e1.record()
+    e1.synchronize()
+    return nbytes * reps / (e0.elapsed_time(e1) * 1e-3)
+
+
 def decode_ceiling(bits: float, device=None, waves: int | None = None, iters: int = 4000) -> float:
     """Decoded weights per second of the register-only decode benchmark (evamx_bench_decode):
     the arithmetic bound of the decode GEMV at ``bits``, timed with events on the current stream."""

@@ -185,6 +185,16 @@ float* evamx_moe_logits_ptr(const evamx_moe_shape* shape, void* workspace);
  * work observable). */
 int evamx_bench_decode(float bits, int waves, int iters, float* sink, evamx_stream_t stream);
 
+/* No counterpart in the reference: a benchmark kernel for the memory-side bound of a decode
+ * GEMV launch. `waves` waves (a multiple of ncg) each read `rows` chunks of 1 KiB (64 lanes x 16
+ * bytes, non-temporal, four in flight): wave w reads byte (w % ncg) * 1024 of rows
+ * (w / ncg) * rows .. + rows - 1 of buf, whose rows are ncg KiB long. With ncg = columns / 128,
+ * rows = the k-slices of one split and waves = the launch's waves this is the bytes of that
+ * launch at 4 bits in its access shape, without the decode. Reads waves * rows KiB, which must
+ * fit in `bytes`; time it with events on `stream`. sink: device float[64] (written only to keep
+ * the loads observable). */
+int evamx_bench_read(const void* buf, size_t bytes, int ncg, int rows, int waves, float* sink, evamx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,6 +132,10 @@ def test_other_entry_points_reject_bad_arguments():
     assert L.evamx_bench_decode(4.0, 4094, 10, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_bench_decode(4.0, 4096, 0, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_bench_decode(4.0, 4096, 10, None, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_bench_read(None, 1 << 20, 16, 4, 16, FAKE, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_bench_read(FAKE, 1 << 20, 16, 4, 24, FAKE, None) == _lib.EVAMX_EINVAL    # waves % ncg
+    assert L.evamx_bench_read(FAKE, 1 << 20, 16, 0, 16, FAKE, None) == _lib.EVAMX_EINVAL    # rows
+    assert L.evamx_bench_read(FAKE, (1 << 20) - 1, 16, 64, 16, FAKE, None) == _lib.EVAMX_EINVAL  # 1 MiB read
     assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7168, 1, FAKE, 256, 7168, None, None) == _lib.EVAMX_EINVAL
     assert L.evamx_router_logits(FAKE, 5, 7168, 1, FAKE, 256, 7168, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_router_logits(FAKE, _lib.DTYPE_BF16, 7168, 1, FAKE, 600, 7168, FAKE, None) == _lib.EVAMX_EINVAL
