@@ -122,6 +122,31 @@ def test_moe_layer_small(dev, rows, K):
     assert np.array_equal(runs, coop.reference_table(ridx, rrw, capacity=16))
 
 
+@pytest.mark.parametrize("rows", [1, 2])
+def test_moe_layer_wide_intermediate(dev, rows):
+    """An intermediate width past DSv3's (I = 2560, 20 activation chunks per row, 5 per k-split
+    of the down GEMV at the defaults) through the decode GEMV path, against the oracle."""
+    ops = _ops()
+    H, I, E, topk, limit, K = 512, 2560, 12, 4, 10.0, 4
+    rng = np.random.default_rng(77 + rows)
+    experts, shared = _layer_case(rng, H, I, E, K, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, rows, H)
+    logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
+    ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+    de = DeviceExperts(experts, dev)
+    ds = DeviceExperts([shared], dev)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), de.table, out, limit=limit, bits=K,
+                    logits=to_dev(logits, dev), sel=sel, weights=w, shared_ptrs=ds.ptrs(0), shared_bits=K)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), ridx)
+    assert int(ws.flags().cpu()[0]) == 0
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+
+
 _DSV3_CASES = {}
 
 
