@@ -834,6 +834,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     gemv_dispatch_k<TMAX>(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
 }
 
+// Fixed-order sums over the k-splits q = 0..S-1 of N values per lane, value n at
+// base[n] + q * stride: each sum adds its splits in q order starting from 0, as a sequential
+// loop does, but the loads of up to QB splits of all N values are issued before any of their
+// adds (one memory round trip per QB splits instead of one per split and value). S is
+// wave-uniform; splits past S are neither loaded nor added.
+template <int N, int QB>
+__device__ __forceinline__ void sum_splits(const float* const (&base)[N], size_t stride, int S, float (&acc)[N])
+{
+#pragma unroll
+    for (int n = 0; n < N; ++n) acc[n] = 0.0f;
+    for (int q0 = 0; q0 < S; q0 += QB) {
+        float t[N][QB];
+#pragma unroll
+        for (int i = 0; i < QB; ++i)
+            if (q0 + i < S)
+#pragma unroll
+                for (int n = 0; n < N; ++n) t[n][i] = gptr<float>(base[n])[(size_t)(q0 + i) * stride];
+#pragma unroll
+        for (int i = 0; i < QB; ++i)
+            if (q0 + i < S)
+#pragma unroll
+                for (int n = 0; n < N; ++n) acc[n] += t[n][i];
+    }
+}
+
 // Activation epilogue: one wave per (grouped row o, 128-chunk a of I). Sums the gate/up
 // partials in fixed order, rounds to fp16 (gu_f32 = false), then exl3_moe_coop_kernel.cuh:
 // 784-805 for routed slots (act_gate with the clamp after SiLU) or the shared expert's EXL3
@@ -860,39 +885,30 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const int Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
                                __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
     const int nslot = moe_nslot(p);
-    // all chunks' partial sums and scales first, so their loads are in flight together
+    // all chunks' scales and partial sums first, so their loads are in flight together
     float g[CPW][2], u[CPW][2], gs[CPW][2], us[CPW][2], ds[CPW][2];
+    const float* base[4 * CPW];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int col = (a0 + c) * 128 + lane_col(lane, h);
-            const float* pg = p.part_gu + (size_t)s * p.I + col;
-            const size_t pstride = (size_t)2 * nslot * p.I;              // next k-split
-            const size_t ustride = (size_t)nslot * p.I;                  // gate -> up
-            float sg = 0.0f, su = 0.0f;
-            int q = 0;
-            for (; q + 4 <= Sg; q += 4) {
-                float tg[4], tu[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    tg[i] = pg[(q + i) * pstride];
-                    tu[i] = pg[(q + i) * pstride + ustride];
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) { sg += tg[i]; su += tu[i]; }
-            }
-            for (; q < Sg; ++q) {
-                sg += pg[q * pstride];
-                su += pg[q * pstride + ustride];
-            }
-            g[c][h] = sg;
-            u[c][h] = su;
             gs[c][h] = h2f(g_svh[col]);
             us[c][h] = h2f(u_svh[col]);
             ds[c][h] = h2f(d_suh[col]);
+            base[4 * c + h] = p.part_gu + (size_t)s * p.I + col;                          // gate
+            base[4 * c + 2 + h] = p.part_gu + (size_t)(nslot + s) * p.I + col;            // up
         }
     }
+    float sums[4 * CPW];
+    sum_splits<4 * CPW, CPW == 1 ? 8 : 2>(base, (size_t)2 * nslot * p.I, Sg, sums);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            g[c][h] = sums[4 * c + h];
+            u[c][h] = sums[4 * c + 2 + h];
+        }
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
         float gg[2], uu[2];
@@ -987,7 +1003,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
 }
 
 // Sum of the down k-split partials of slot s on this lane's two columns, fixed order; loads of
-// four splits are issued before their adds.
+// four splits are issued before their adds. (sum_splits here was slower in the combine
+// kernels: 9.2 -> 9.9 us at 16 tokens, 85 -> 110 us at 512.)
 __device__ __forceinline__ void sum_partials(const MoeParams& p, int s, int cg, int lane, int S, float (&v)[2])
 {
     const size_t stride = (size_t)moe_nslot(p) * p.H;
