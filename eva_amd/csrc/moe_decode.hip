@@ -1228,30 +1228,24 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     } else {
         // Chunks hold at most min(T, EVAMX_CHUNK) rows: each token picks an expert once, and the
         // shared expert's chunks are cut at EVAMX_CHUNK rows (repeated picks are handled in the GEMV).
-        const int tmax = tmax_for(p.T < EVAMX_CHUNK ? p.T : EVAMX_CHUNK);
+        // the decode GEMV serves calls below EVAMX_MFMA_MIN_ROWS rows: one- and two-row variants
+        // (a chunk with more rows, from routes that repeat an expert, runs two rows at a time)
+        const int tmax = p.T <= 1 ? 1 : 2;
         {
             // one wave per item: a requested split gives every chunk exactly ks_gu splits, an
             // automatic one fits the resident grid (moe_ksplit)
             const long units = (long)EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128) * (p.ks_gu > 0 ? p.ks_gu : 1);
             const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
             const half_t* xr = p.xr;
-            switch (tmax) {
-                case 1: launch_timed(moe_gate_up_kernel<1>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
-                case 2: launch_timed(moe_gate_up_kernel<2>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
-                case 4: launch_timed(moe_gate_up_kernel<4>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
-                default: launch_timed(moe_gate_up_kernel<8>, grid, dim3(256), stream, ev(2), ev(3), p, xr); break;
-            }
+            if (tmax == 1) launch_timed(moe_gate_up_kernel<1>, grid, dim3(256), stream, ev(2), ev(3), p, xr);
+            else launch_timed(moe_gate_up_kernel<2>, grid, dim3(256), stream, ev(2), ev(3), p, xr);
         }
         launch_act(p, nslot, stream, ev(4), ev(5));
         const long units = (long)EVAMX_MAX_MULT * p.max_chunks * (p.H / 128) * (p.ks_d > 0 ? p.ks_d : 1);
         const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
         const half_t* act = p.act;
-        switch (tmax) {
-            case 1: launch_timed(moe_down_kernel<1>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
-            case 2: launch_timed(moe_down_kernel<2>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
-            case 4: launch_timed(moe_down_kernel<4>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
-            default: launch_timed(moe_down_kernel<8>, grid, dim3(256), stream, ev(6), ev(7), p, act); break;
-        }
+        if (tmax == 1) launch_timed(moe_down_kernel<1>, grid, dim3(256), stream, ev(6), ev(7), p, act);
+        else launch_timed(moe_down_kernel<2>, grid, dim3(256), stream, ev(6), ev(7), p, act);
     }
     if (p.T <= EVAMX_SMALL_ROWS) {
         int nw = p.topk + (p.has_shared ? 1 : 0);
