@@ -211,8 +211,8 @@ def parse_args():
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, "
-              "'How the path would shard'); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the expert path "
+              "shards by experts across GPUs, which one GPU cannot show); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch

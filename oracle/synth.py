@@ -1,10 +1,10 @@
-"""Seeded synthetic inputs for the BASELINE configurations (test infrastructure; numpy).
+"""Seeded synthetic inputs for the benchmark configurations (test infrastructure; numpy).
 
 The GPU tests generate inputs here, upload them, and compare against the oracle on the
 same arrays. ``bench.py`` generates its (much larger) inputs on the device with the same
 distributions; parity at those sizes is checked through size-independent properties.
 
-Distributions:
+Distributions of the benchmark configurations:
 
 - trellis: uniform int16 over all 65 536 values, ``[in/16, out/16, T]``;
 - suh: Rademacher +-1 (fp16); svh: +-1 * U(0.5, 1.5) * svh_scale (fp16);
