@@ -93,7 +93,7 @@ def _layer_case(rng, H, I, E, K, svh_scale, rates=None):
     return experts, shared
 
 
-@pytest.mark.parametrize("rows", [1, 2, 5, 16])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 16])
 @pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
 def test_moe_layer_small(dev, rows, K):
     ops = _ops()
@@ -220,6 +220,30 @@ def test_moe_mixed_rates_and_given_routes(dev, rate_set):
     ops.moe_forward(ws, to_dev(x, dev), de.table, out, limit=limit, k2_per_expert=de.k2,
                     sel=to_dev(sel, dev), rw=to_dev(rw, dev))
     torch.cuda.synchronize()
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3])
+def test_moe_given_routes_repeating_an_expert(dev, rows):
+    """Given routes may name one expert in several slots of a token (the runner passes them
+    through); every slot is its own product, so an expert's chunk holds more rows than there are
+    tokens: the one- and two-row decode GEMVs walk them in groups, the MFMA tiles take them as
+    rows."""
+    ops = _ops()
+    H, I, E, topk, limit = 256, 256, 5, 8, 0.0
+    rng = np.random.default_rng(300 + rows)
+    experts, _ = _layer_case(rng, H, I, E, 4, 1 / np.sqrt(H))
+    x = rng.standard_normal((rows, H)).astype(np.float16)
+    sel = rng.integers(0, E, size=(rows, topk)).astype(np.int64)      # 8 picks of 5 experts
+    sel[0, :4] = 2                                                    # one expert in 4 slots
+    rw = rng.uniform(0.1, 1.0, size=(rows, topk)).astype(np.float16)
+    ref = coop.moe_routed(x, sel, rw, experts, limit)
+    de = DeviceExperts(experts, dev)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=False)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev), de.table, out, limit=limit, bits=4, sel=to_dev(sel, dev), rw=to_dev(rw, dev))
+    torch.cuda.synchronize()
+    assert int(ws.flags().cpu()[0]) == 0
     assert rel_err_rows(out.cpu().numpy(), ref) < TOL
 
 
