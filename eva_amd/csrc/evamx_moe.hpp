@@ -134,9 +134,15 @@ __device__ __forceinline__ int split_waves(const MoeParams& p)
     return (!p.mfma && p.T == 1) ? p.gemv_waves / 2 : p.gemv_waves;
 }
 
+// MFMA gate/up tiles that leave part of one resident round empty unsplit take two splits: with
+// items < waves per split, SIMDs hold 3 or 4 equal items, and the ones with 4 set the launch's
+// time; two splits even that out (16 tokens at DSv3: gate/up 228-230 -> 224-225 us).
 __device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
 {
-    return moe_ksplit(p.ks_gu, units * 2 * (p.I / 128), split_waves(p), p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
+    const int items = units * 2 * (p.I / 128);
+    KSplit k = moe_ksplit(p.ks_gu, items, split_waves(p), p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
+    if (p.mfma && p.ks_gu == 0 && k.base == 1 && items < split_waves(p) && k.cap >= 2) k.base = 2;
+    return k;
 }
 
 __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)

@@ -294,7 +294,8 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     const int kreq = which == 0 ? p.ks_gu : p.ks_d;
     const int kmax = which == 0 ? p.ks_gu_max : p.ks_d_max;
     const long per_tile = (long)(which == 0 ? 2 * ncg : ncg);
-    const long auto_items = (long)p.gemv_waves + per_tile;   // an automatic split fills one resident round
+    // an automatic split fills one resident round (gate/up: up to two, see ks_gate_up)
+    const long auto_items = (long)(which == 0 ? 2 : 1) * p.gemv_waves + per_tile;
     const long items = kreq > 0 ? (long)p.max_chunks * per_tile * kreq
                                 : (p.max_chunks * per_tile > auto_items ? (long)p.max_chunks * per_tile : auto_items);
     long blocks = (items + MF_WAVES - 1) / MF_WAVES;
