@@ -605,8 +605,9 @@ def read_floor(torch, ops, H, I, units, achieved_gbps):
     in its own shape, without the decode. One-row calls aim their k-split at two waves per SIMD:
     units x (gate, up) x I/128 column groups x ks waves, ks = that target over the per-split
     items, each wave streaming the 8 * (H/128 / ks) k-slices of its split as 1 KiB chunks (8 tiles
-    at 4 bits), four in flight. Back-to-back launches, so the figure includes each launch's ramp
-    and tail but only part of the gap between launches."""
+    at 4 bits), four in flight. Back-to-back launches over distinct copies of at least 1 GiB in
+    total (a repeated 132 MB buffer would be served partly by the Infinity Cache), so the figure
+    includes each launch's ramp and tail but only part of the gap between launches."""
     ncg = I // 128
     per_split = units * 2 * ncg
     waves_target = torch.cuda.get_device_properties(0).multi_processor_count * 16 // 2

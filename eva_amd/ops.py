@@ -274,18 +274,28 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
 def read_floor(ncg: int, rows: int, waves: int, device=None, reps: int = 50) -> float:
     """Bytes per second of the read-only benchmark (evamx_bench_read): ``waves`` waves stream
     ``rows`` 1 KiB chunks each in a decode GEMV launch's shape (wave w reads column group w % ncg
-    of its chain's rows), no decode; ``reps`` back-to-back launches timed with events."""
+    of its chain's rows), no decode; ``reps`` back-to-back launches timed with events. The
+    launches cycle through distinct copies totalling at least 1 GiB, as the layer benchmark
+    cycles its weights, so that the 256 MiB Infinity Cache cannot serve a repeated buffer."""
     dev = torch.device("cuda", 0) if device is None else torch.device(device)
     nbytes = (waves // ncg) * rows * ncg * 1024
-    buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    copies = min(64, max(2, -(-(1 << 30) // nbytes)))
+    buf = torch.zeros(copies * nbytes, dtype=torch.uint8, device=dev)
     sink = torch.zeros(64, dtype=torch.float32, device=dev)
     stream = stream_handle(dev)
-    check(lib().evamx_bench_read(ptr(buf), nbytes, ncg, rows, waves, ptr(sink), stream), "evamx_bench_read")   # warm-up
+    base = ptr(buf)
+
+    def launch(i):
+        check(lib().evamx_bench_read(base + (i % copies) * nbytes, nbytes, ncg, rows, waves, ptr(sink), stream),
+              "evamx_bench_read")
+
+    for i in range(copies):   # warm-up: every copy once
+        launch(i)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        check(lib().evamx_bench_read(ptr(buf), nbytes, ncg, rows, waves, ptr(sink), stream), "evamx_bench_read")
+    for i in range(reps):
+        launch(i)
     e1.record()
     e1.synchronize()
     return nbytes * reps / (e0.elapsed_time(e1) * 1e-3)

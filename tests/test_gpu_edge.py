@@ -162,3 +162,12 @@ def test_decode_ceiling_benchmark(dev):
     for bits in (1.5, 2.0, 2.5, 3.0, 3.5, 4.0, 5.0):
         wps = ops.decode_ceiling(bits, dev, iters=200)
         assert 1e12 < wps < 1e14, (bits, wps)
+
+
+def test_read_floor_benchmark(dev):
+    """The read-only benchmark runs in a small and in the one-row gate/up shape and reports a rate
+    below HBM's 8 TB/s peak (the buffers are far larger than the caches at the full shape)."""
+    from eva_amd import ops
+    assert ops.read_floor(16, 8, 64, dev, reps=3) > 0
+    bps = ops.read_floor(16, 64, 2016, dev, reps=5)
+    assert 1e12 < bps < 8.5e12, bps
