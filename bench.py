@@ -80,6 +80,7 @@ class DeviceLayers:
         self.rates = [[float(rate_of(l, e)) if e < n_experts or sb is None else sb for e in range(self.n)]
                       for l in range(n_layers)]
         tiles_gu = (hidden // 16) * (inter // 16)        # tiles per projection (all three equal)
+        self.tiles_gu, self.hidden, self.inter = tiles_gu, hidden, inter
         offs, total = [], 0
         for l in range(n_layers):
             row = []
@@ -87,6 +88,7 @@ class DeviceLayers:
                 row.append(total)
                 total += 3 * tiles_gu * tile_u16(self.rates[l][e])
             offs.append(row)
+        self.offs = offs
         log(f"allocating {total * 2 / 1e9:.1f} GB of trellis for {n_layers} layer(s)")
         self.trellis = torch.empty(total, dtype=torch.int16, device=dev)
         chunk = 1 << 28
@@ -122,6 +124,20 @@ class DeviceLayers:
             self.k2.append(torch.tensor([int(round(2 * r)) for r in self.rates[l][:n_experts]],
                                         dtype=torch.uint8, device=dev) if self.mixed else None)
 
+    def expert_parts(self, torch, l, e):
+        """Host copies of expert e of layer l (e = -1: the shared expert):
+        ((trellis, suh, svh) for gate, up, down) as CPU tensors, exactly the bytes the GPU reads."""
+        e = self.n - 1 if e < 0 else e
+        tu = tile_u16(self.rates[l][e])
+        pe = self.tiles_gu * tu
+        parts = []
+        for p, (n_in, n_out) in enumerate(((self.hidden, self.inter), (self.hidden, self.inter),
+                                           (self.inter, self.hidden))):
+            t0 = self.offs[l][e] + p * pe
+            tr = self.trellis[t0:t0 + pe].view(n_in // 16, n_out // 16, tu).cpu()
+            parts.append((tr, self.suh[l, e, p, :n_in].cpu(), self.svh[l, e, p, :n_out].cpu()))
+        return tuple(parts)
+
     def step_bytes(self, l, experts):
         """Algorithmic weight bytes of layer l for the given routed experts plus the shared one."""
         return sum(expert_bytes(self.rates[l][e]) for e in experts) + expert_bytes(self.rates[l][-1])
@@ -130,46 +146,195 @@ class DeviceLayers:
         return sum(2 * proj_bytes(H, I, self.rates[l][e]) for e in list(experts) + [self.n - 1])
 
 
-def cpu_baseline(bits=4.0, tokens=1, n_routed=1, min_seconds=10.0):
-    """PyTorch-CPU restatement on the host cores: ``n_routed`` routed experts + the shared
-    expert of a ``tokens``-token layer at ``bits`` (a bounded sample of the GPU workload)."""
-    import numpy as np
-    import torch
+def cpu_info(torch):
+    """Host description for the CPU baseline: lscpu's model name, torch version and threading."""
+    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), "")
+    except Exception:
+        pass
+    if not model:
+        try:
+            model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+        except Exception:
+            pass
+    return {"cpu_model": model, "torch": torch.__version__, "torch_threads": torch.get_num_threads(),
+            "mkl": bool(torch.backends.mkl.is_available()), "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
 
-    from oracle import synth, torch_cpu
+
+def cpu_baseline(torch, layers, l, x_dev, logits_dev, tokens, limit, what):
+    """The PyTorch-CPU restatement (oracle/torch_cpu.py) on the host cores, on the GPU step's own
+    inputs: the first ``tokens`` rows of the step's activations (cast to fp16 as Block.experts
+    does) and logits, routed on the CPU (sigmoid top-8), through the experts of layer ``l``
+    copied from HBM (the routed experts those tokens pick and the shared expert). 2 warm-ups,
+    then the median of 5 runs; GB/s over the same algorithmic bytes as the GPU line."""
+    from oracle import torch_cpu
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    rng = np.random.default_rng(5)
-    ew = [synth.expert(rng, H, I, bits, 1 / np.sqrt(H)) for _ in range(n_routed + 1)]
-    parts = [tuple(tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in ew_i.parts[p]) for p in "gud") for ew_i in ew]
-    dec = torch_cpu.Decoder(bits)
-    x = torch.from_numpy(synth.activations_bf16(rng, tokens, H))
-    idx = torch.tensor([[e for e in range(n_routed)]] * tokens)
-    w = torch.full((tokens, n_routed), 1.0 / n_routed)
-    experts = {e: parts[e] for e in range(n_routed)}
+    x = x_dev[:tokens].float().cpu().half().float()
+    z = logits_dev[:tokens].float().cpu()
+    idx, _ = torch_cpu.route_sigmoid(z, TOPK)
+    used = sorted(set(idx.reshape(-1).tolist()))
+    experts = {e: layers.expert_parts(torch, l, e) for e in used}
+    shared = layers.expert_parts(torch, l, -1)
+    decs = {}
+    for e in used + [-1]:
+        rate = layers.rates[l][e if e >= 0 else layers.n - 1]
+        decs.setdefault(rate, torch_cpu.Decoder(rate))
+    dec = {e: decs[layers.rates[l][e if e >= 0 else layers.n - 1]] for e in used + [-1]}
 
     def run():
-        return torch_cpu.moe_layer(x, idx, w, experts, parts[n_routed], dec, 10.0)
+        i, w = torch_cpu.route_sigmoid(z, TOPK)
+        return torch_cpu.moe_layer(x, i, w, experts, shared, dec, limit)
 
-    run()                                   # warm-up
+    for _ in range(2):
+        run()
     times = []
-    while len(times) < 2 or (sum(times) < min_seconds and len(times) < 12):
+    for _ in range(5):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    t = sum(times) / len(times)
-    nbytes = (n_routed + 1) * expert_bytes(bits)
-    model = ""
-    try:
-        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except Exception:
-        pass
-    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{n_routed} routed + 1 shared expert of a {tokens}-token DSv3 layer at {bits:g} bpw "
-                      f"({nbytes / 1e6:.1f} MB; mean of {len(times)} runs after 1 warm-up; {t:.2f} s each, "
-                      f"{sum(times):.1f} s timed)",
-            "seconds_per_sample": round(t, 3), "cpu_model": model, "torch_threads": torch.get_num_threads()}
+    t = sorted(times)[2]
+    nbytes = layers.step_bytes(l, used) + tokens * (H * 2 + E * 4 + H * 4)
+    res = {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+           "sample": f"{what}: {tokens} token(s), {len(used)} routed experts + the shared expert of layer {l} "
+                     f"({nbytes / 1e6:.1f} MB), routing included; median of 5 runs after 2 warm-ups "
+                     f"({t:.2f} s per run)",
+           "seconds_per_sample": round(t, 3), "runs_s": [round(v, 3) for v in times]}
+    res.update(cpu_info(torch))
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# rocprofv3 CSV -> markdown summaries (the tables under profiles/ are printed by these).
+
+STAGES = (("prepare", ("moe_prepare", "moe_route", "moe_group", "moe_rotate", "moe_gate_kernel")),
+          ("gate/up", ("moe_gate_up",)), ("act", ("moe_act",)), ("down", ("moe_down",)),
+          ("combine", ("moe_combine",)))
+
+
+def kernel_short_name(name):
+    """'void evamx::moe_gate_up_mfma_kernel<1>(evamx::MoeParams)' -> 'moe_gate_up_mfma_kernel<1>'."""
+    import re
+    n = name.strip()
+    m = re.match(r"_ZN5evamx(\d+)", n)          # left mangled by the profiler: length-prefixed name
+    if m:
+        i = m.end()
+        ident = n[i:i + int(m.group(1))]
+        targs = re.match(r"I((?:Li-?\d+E)+)E", n[i + len(ident):])
+        if targs:
+            ident += "<" + ", ".join(re.findall(r"Li(-?\d+)E", targs.group(1))) + ">"
+        return ident
+    if n.startswith("void "):
+        n = n[5:]
+    depth, cut = 0, len(n)
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    n = n[:cut]
+    return re.sub(r"^(evamx::|at::native::|\(anonymous namespace\)::)+", "", n)
+
+
+def stage_of(short):
+    for stage, prefixes in STAGES:
+        if short.startswith(prefixes):
+            return stage
+    return None
+
+
+def summarize_trace(path, skip=0):
+    """Per-kernel dispatch count and durations (µs) of a rocprofv3 --kernel-trace CSV, evamx
+    kernels only, after dropping each kernel's first ``skip`` dispatches (warm-up), and the sum
+    per forward of each MoE stage (forwards = dispatches of the combine stage)."""
+    import csv
+    import collections
+    durs = collections.defaultdict(list)
+    for row in csv.DictReader(open(path)):
+        short = kernel_short_name(row["Kernel_Name"])
+        if not row["Kernel_Name"].strip().startswith(("void evamx::", "evamx::", "_ZN5evamx")):
+            continue
+        durs[short].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    lines = ["| kernel | dispatches | avg µs | median µs | min µs | max µs |", "|---|---|---|---|---|---|"]
+    stage_tot = collections.defaultdict(float)
+    n_fwd = 0
+    for k in sorted(durs):
+        d = durs[k][skip:] or durs[k]
+        lines.append(f"| {k} | {len(d)} | {sum(d) / len(d):.2f} | {median(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
+        st = stage_of(k)
+        if st:
+            stage_tot[st] += sum(d)
+        if st == "combine":
+            n_fwd += len(d)
+    if n_fwd:
+        lines += ["", f"per forward ({n_fwd} forwards): " + ", ".join(
+            f"{st} {stage_tot[st] / n_fwd:.2f} µs" for st, _ in STAGES if st in stage_tot)]
+    return "\n".join(lines)
+
+
+def _pmc_rows(path):
+    import csv
+    import collections
+    vals = collections.defaultdict(lambda: collections.defaultdict(float))
+    for row in csv.DictReader(open(path)):
+        key = (kernel_short_name(row["Kernel_Name"]), int(row["Dispatch_Id"]))
+        vals[row["Counter_Name"]][key] += float(row["Counter_Value"])
+    return vals
+
+
+def summarize_pmc(paths, calib_paths, copy_bytes=1 << 30, key=None):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of rocprofv3 --pmc CSVs, each counter scaled by
+    the factor that makes the copy kernel of ``calib_paths`` (``bench.py --copy-calibration``:
+    ``copy_bytes`` read and written per dispatch) read and write exactly that; per evamx kernel
+    and per MoE stage and forward. With ``key`` also prints the gate/up stage's bytes per forward
+    as ``traffic_bytes_per_launch[key]: N`` (the line bench.py reads)."""
+    import collections
+    factor = {}
+    lines = ["| counter | copy kernel KiB per dispatch | expected KiB | scale factor |", "|---|---|---|---|"]
+    for cp in calib_paths:
+        for counter, per in _pmc_rows(cp).items():
+            v = [x for (k, _), x in per.items() if "copyBuffer" in k]
+            if v:
+                kib = sum(v) / len(v)
+                factor[counter] = copy_bytes / 1024 / kib
+                lines.append(f"| {counter} | {kib:.0f} | {copy_bytes // 1024} | {factor[counter]:.4f} |")
+    per_kernel = collections.defaultdict(dict)
+    for p in paths:
+        for counter, per in _pmc_rows(p).items():
+            by_k = collections.defaultdict(list)
+            for (k, _), x in per.items():
+                if stage_of(k):
+                    by_k[k].append(x)
+            for k, xs in by_k.items():
+                per_kernel[k][counter] = xs
+    counters = sorted({c for d in per_kernel.values() for c in d})
+    lines += ["", "| kernel | dispatches | " + " | ".join(f"{c} KiB" for c in counters) + " | "
+              + " | ".join(f"scaled {c} MB" for c in counters) + " |",
+              "|---|---|" + "---|" * (2 * len(counters))]
+    stage_bytes = collections.defaultdict(float)
+    n_fwd = 0
+    for k in sorted(per_kernel):
+        d = per_kernel[k]
+        n = max(len(v) for v in d.values())
+        avg = {c: sum(d[c]) / len(d[c]) for c in d}
+        lines.append(f"| {k} | {n} | " + " | ".join(f"{avg.get(c, 0):.0f}" for c in counters) + " | "
+                     + " | ".join(f"{avg.get(c, 0) * 1024 * factor.get(c, 1.0) / 1e6:.2f}" for c in counters) + " |")
+        st = stage_of(k)
+        stage_bytes[st] += sum(sum(d[c]) * 1024 * factor.get(c, 1.0) for c in d)
+        if st == "combine":
+            n_fwd = max(n_fwd, n)
+    if n_fwd:
+        lines += ["", f"HBM bytes per forward by stage (scaled counters summed, {n_fwd} forwards): " + ", ".join(
+            f"{st} {stage_bytes[st] / n_fwd:.0f}" for st, _ in STAGES if st in stage_bytes)]
+        if key:
+            lines.append(f"traffic_bytes_per_launch[{key}]: {stage_bytes['gate/up'] / n_fwd:.0f}")
+    return "\n".join(lines)
 
 
 def parse_args():
@@ -197,6 +362,14 @@ def parse_args():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (the reference kernel for FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print the markdown summary of a rocprofv3 kernel_trace.csv and exit (no GPU)")
+    ap.add_argument("--summarize-pmc", metavar="CSV", nargs="+",
+                    help="print the markdown summary of rocprofv3 --pmc counter_collection.csv files and exit")
+    ap.add_argument("--calibration", metavar="CSV", nargs="*", default=[],
+                    help="with --summarize-pmc: the counter CSVs of a --copy-calibration run")
+    ap.add_argument("--traffic-key", default=None, help="with --summarize-pmc: e.g. tokens=1,bits=4")
+    ap.add_argument("--skip-dispatches", type=int, default=0, help="with --summarize-trace: warm-up dispatches")
     args = ap.parse_args()
     defaults = {"layer": (1, 4.0, 4), "stack": (8, 2.5, 58), "prefill": (512, None, 2), "linear": (1, 4.0, 64)}[args.workload]
     if args.tokens is None:
@@ -210,6 +383,12 @@ def parse_args():
 
 def main():
     args = parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.skip_dispatches))
+        return
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc, args.calibration, key=args.traffic_key))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the expert path "
               "shards by experts across GPUs, which one GPU cannot show); run with --gpus 1", file=sys.stderr)
@@ -266,16 +445,39 @@ def make_logits(torch, g, dev, n_draws, T, routing):
     return logits
 
 
-def timed_replays(torch, stream, run_block, reps, warm):
-    run_block(warm)
+MIN_REPLAYS = 20
+
+
+def timed_replays(torch, stream, replay, n, warm):
+    """``warm`` untimed calls of ``replay`` (one graph replay), then ``n`` timed ones on
+    ``stream``, each between its own pair of consecutive events. Returns (ms of each replay, ms
+    of all n from the first event to the last)."""
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            replay()
     torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    run_block(reps)
-    ev1.record(stream)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    with torch.cuda.stream(stream):
+        evs[0].record(stream)
+        for i in range(n):
+            replay()
+            evs[i + 1].record(stream)
     torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1)
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(n)], evs[0].elapsed_time(evs[n])
+
+
+def median(v):
+    v = sorted(v)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+
+
+def replay_stats(ms, steps_per_replay):
+    """Per-step figures from per-replay times: the median (the reported value), the mean over
+    the whole timed region, and the spread."""
+    per = [m / steps_per_replay for m in ms]
+    return {"replays": len(ms), "steps_per_replay": steps_per_replay, "median_ms": median(per),
+            "mean_ms": sum(per) / len(per), "min_ms": min(per), "max_ms": max(per)}
 
 
 def run_layer(torch, args):
@@ -337,24 +539,25 @@ def run_layer(torch, args):
             with torch.cuda.graph(graph, stream=stream):
                 for i in range(G):
                     step(i)
-    reps = max(1, args.steps // G)
+    # at least --steps steps, in at least MIN_REPLAYS replays of G steps each
+    reps = max(MIN_REPLAYS, -(-args.steps // G))
     steps = reps * G
     step_bytes = sum(layers.step_bytes(i % args.layers, touched[i % n_draws]) for i in range(G)) / G + act_bytes
     mean_uniq = sum(len(touched[i % n_draws]) for i in range(G)) / G
 
-    def run_block(n):
-        with torch.cuda.stream(stream):
-            if graph is not None:
-                for _ in range(n):
-                    graph.replay()
-            else:
-                for i in range(n * G):
-                    step(i)
+    def replay():
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(G):
+                step(i)
 
-    ms = timed_replays(torch, stream, run_block, reps, max(1, args.warmup // G))
-    us_step = ms * 1e3 / steps
+    ms, total_ms = timed_replays(torch, stream, replay, reps, max(1, -(-args.warmup // G)))
+    st = replay_stats(ms, G)
+    us_step = st["median_ms"] * 1e3
     gbps = step_bytes / (us_step * 1e-6) / 1e9
-    log(f"{steps} steps, {us_step:.2f} us/step, {gbps:.1f} GB/s (unique experts/step {mean_uniq:.1f})")
+    log(f"{steps} steps in {reps} replays: median {us_step:.2f} us/step (mean {st['mean_ms'] * 1e3:.2f}), "
+        f"{gbps:.1f} GB/s (unique experts/step {mean_uniq:.1f})")
 
     # Per-kernel durations on the launch stream (eager pass, events between the launches).
     n_ev = 16 if prefill else 64
@@ -378,6 +581,7 @@ def run_layer(torch, args):
     result = {
         "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 6), "us_per_layer": round(us_step, 3),
+        "timing": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in st.items()},
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5)/sqrt(H) svh, N(0,1) logits, bf16 N(0,1) x)",
         "config": {"workload": f"DSv3 MoE layer {'prefill' if prefill else 'decode'}, {T} token(s), {rates} EXL3 "
@@ -392,10 +596,8 @@ def run_layer(torch, args):
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        if prefill:
-            result["cpu_baseline"] = cpu_baseline(bits=4.0, tokens=16, n_routed=1)
-        else:
-            result["cpu_baseline"] = cpu_baseline(bits=args.bits, tokens=T, n_routed=1)
+        what = f"step 0 of the timed sequence (layer 0, routing draw 0){'' if T == 1 else f', first token of {T}'}"
+        result["cpu_baseline"] = cpu_baseline(torch, layers, 0, x, logits[0], 1, 10.0, what)
     return result
 
 
@@ -443,20 +645,17 @@ def run_stack(torch, args):
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
             step()
-    steps = max(1, args.steps // 20)
+    steps = max(MIN_REPLAYS, args.steps)       # one replay = one step through the L layers
 
-    def run_block(n):
-        with torch.cuda.stream(stream):
-            for _ in range(n):
-                graph.replay()
-
-    ms = timed_replays(torch, stream, run_block, steps, max(1, args.warmup // 20))
-    ms_step = ms / steps
+    ms, total_ms = timed_replays(torch, stream, graph.replay, steps, max(1, min(args.warmup, 5)))
+    st = replay_stats(ms, 1)
+    ms_step = st["median_ms"]
     gbps = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"{steps} graph replays of {L} layers: {ms_step:.3f} ms/step, {gbps:.1f} GB/s "
-        f"(unique experts/layer {mean_uniq:.1f})")
+    log(f"{steps} graph replays of {L} layers: median {ms_step:.3f} ms/step (mean {st['mean_ms']:.3f}), "
+        f"{gbps:.1f} GB/s (unique experts/layer {mean_uniq:.1f})")
     ref = h.clone()
-    run_block(1)
+    with torch.cuda.stream(stream):
+        graph.replay()
     torch.cuda.synchronize()
     if not torch.equal(ref, h):
         raise RuntimeError("graph replays of the stacked step are not deterministic")
@@ -468,6 +667,7 @@ def run_stack(torch, args):
     result = {
         "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "us_per_layer": round(ms_step * 1e3 / L, 3),
+        "timing": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in st.items()},
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5)/sqrt(H) svh, N(0,1) logits, bf16 N(0,1) h)",
         "config": {"workload": f"DSv3 expert-only decode step, {L} stacked layers, {T} tokens, {K:g} bpw EXL3, "
@@ -482,7 +682,8 @@ def run_stack(torch, args):
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(bits=K, tokens=T, n_routed=1)
+        result["cpu_baseline"] = cpu_baseline(torch, layers, 0, h0, logits[0], 1, 10.0,
+                                              "layer 0 of the stacked step, first token of 8")
     return result
 
 
@@ -520,17 +721,10 @@ def run_linear(torch, args):
             for i in range(copies):
                 call(i)
     eager = out.clone()
-    reps = max(1, args.steps // copies)
-    with torch.cuda.stream(stream):
-        for _ in range(max(1, args.warmup // copies)):
-            graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        for _ in range(reps):
-            graph.replay()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / (reps * copies)
+    reps = max(MIN_REPLAYS, -(-args.steps // copies))
+    ms, total_ms = timed_replays(torch, stream, graph.replay, reps, max(1, -(-args.warmup // copies)))
+    st = replay_stats(ms, copies)
+    dt = st["median_ms"] * 1e-3
     if not torch.equal(out, eager):
         raise RuntimeError("graph replays differ from the eager calls")
     nbytes = n_in * n_out * bits / 8 + 2 * (n_in + n_out) + T * 2 * (n_in + n_out)
@@ -538,7 +732,8 @@ def run_linear(torch, args):
     result = {
         "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": reps * copies, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 6),
-        "us_per_call": round(dt * 1e6, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "us_per_call": round(dt * 1e6, 3),
+        "timing": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in st.items()}, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16", "data": "synthetic (seeded uniform trellis, +-1 suh, +-U(0.5,1.5) svh, bf16 N(0,1) x)",
         "config": {"workload": f"single EXL3 linear {n_in} -> {n_out}, {bits:g} bpw, {T} token(s), "
                                f"{copies} resident copies in one graph (BASELINE configs[0])",
@@ -548,34 +743,37 @@ def run_linear(torch, args):
                      "peak": PEAK_HBM, "unit": "GB/s", "frac": round(gbps / PEAK_HBM, 4), "traffic": None},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_linear_baseline(torch, n_in, n_out, bits, T)
+        result["cpu_baseline"] = cpu_linear_baseline(torch, x, trellis[0], suh[0], svh[0], bits)
     return result
 
 
-def cpu_linear_baseline(torch, n_in, n_out, bits, T, min_seconds=10.0):
-    """The PyTorch-CPU restatement of the same linear (LUT decode, H128 matmuls, fp32 product)."""
-    import numpy as np
-
-    from oracle import synth, torch_cpu
+def cpu_linear_baseline(torch, x_dev, trellis_dev, suh_dev, svh_dev, bits):
+    """The PyTorch-CPU restatement of the same linear on the GPU run's own inputs (copy 0 of the
+    resident weights, the same activations): LUT decode, H128 matmuls, fp32 product. 2 warm-ups,
+    then the median of 5 runs."""
+    from oracle import torch_cpu
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    rng = np.random.default_rng(5)
-    tr, suh, svh = (torch.from_numpy(np.ascontiguousarray(a)) for a in synth.projection(rng, n_in, n_out, bits))
+    tr, suh, svh = trellis_dev.cpu(), suh_dev.cpu(), svh_dev.cpu()
+    x = x_dev.float().cpu()
     dec = torch_cpu.Decoder(bits)
-    x = torch.from_numpy(synth.activations_bf16(rng, T, n_in))
-    torch_cpu.linear_forward(x, tr, suh, svh, dec)
+    for _ in range(2):
+        torch_cpu.linear_forward(x, tr, suh, svh, dec)
     times = []
-    while len(times) < 2 or (sum(times) < min_seconds and len(times) < 50):
+    for _ in range(5):
         t0 = time.perf_counter()
         torch_cpu.linear_forward(x, tr, suh, svh, dec)
         times.append(time.perf_counter() - t0)
-    t = sum(times) / len(times)
-    nbytes = n_in * n_out * bits / 8 + 2 * (n_in + n_out)
-    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"the same {n_in} -> {n_out} linear at {bits:g} bpw, {T} token(s) (mean of {len(times)} runs "
-                      f"after 1 warm-up; {t * 1e3:.1f} ms each)",
-            "seconds_per_sample": round(t, 4), "torch_threads": torch.get_num_threads()}
+    t = sorted(times)[2]
+    n_in, n_out = suh.numel(), svh.numel()
+    nbytes = n_in * n_out * bits / 8 + 2 * (n_in + n_out) + x.shape[0] * 2 * (n_in + n_out)
+    res = {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+           "sample": f"copy 0 of the GPU run's {n_in} -> {n_out} linear at {bits:g} bpw on its {x.shape[0]} token(s); "
+                     f"median of 5 runs after 2 warm-ups ({t * 1e3:.1f} ms per run)",
+           "seconds_per_sample": round(t, 4), "runs_s": [round(v, 4) for v in times]}
+    res.update(cpu_info(torch))
+    return res
 
 
 def gate_up_roofline(bytes_launch, us, traffic):

@@ -5,10 +5,11 @@ Mirrors the reference's Python interface so callers switch by import:
 - ``CoopRunner(device, topk, hidden, inter, rows=1).run(x, sel, weights, packed, k, limit)``
   -> borrowed fp32 ``[rows, hidden]`` (runtime/ds41/moe_coop.py:15-69);
 - ``CoopRunner512/2048/3072(device, topk=6, hidden=5120, inter=2304, max_rows=...)`` with
-  ``run(..., check_bounds=True)`` -> owned fp32 ``[M, hidden]``, ``prepare_routes``,
+  ``run(..., check_bounds=True)`` -> fp32 ``[M, hidden]``, ``prepare_routes``,
   ``run_table``, ``lifecycle``, ``close`` (runtime/ds41/moe_coop3072.py:261-402,
   moe_coop512.py:170-253, moe_coop2048.py:220-351), with their ownership rules: one owner
   thread, the construction stream, a non-blocking lock, and any failure poisons the runner.
+  CoopRunner512 returns the runner's own output rows (borrowed), as moe_coop512.py:248 does.
 
 Generalised as the DeepSeek-V3 shapes need: any hidden/inter (multiples of 128), top-k up to
 32, up to 512 local experts, rates 1.5 to 4 bits in steps of 0.5 and 5 bits. ``packed`` is the ``[9, n_local]`` int64
@@ -26,6 +27,7 @@ Differences, all on the side of fewer host round trips:
 """
 from __future__ import annotations
 
+import contextlib
 import math
 import threading
 
@@ -109,11 +111,94 @@ class CoopRunner:
         return self.out
 
 
+class _Ownership:
+    """The reference runners' usage contract (moe_coop3072.py:261-402) as one guard: calls come
+    from the thread that built the runner, on the stream that was current then, one at a time
+    (a second concurrent call is refused, not queued); an exception inside a guarded call
+    poisons the runner for good; once closed it accepts nothing. ``leases`` keeps the tensors a
+    failed call had handed to the GPU alive until a successful close has drained the stream."""
+
+    def __init__(self, device):
+        self.device = device
+        self.stream = torch.cuda.current_stream(device)
+        self.tid = threading.get_ident()
+        self.busy = threading.Lock()
+        self.poisoned = False
+        self.shut = False
+        self.drains = 0
+        self.leases = []
+
+    def on_owner_thread(self):
+        return threading.get_ident() == self.tid
+
+    @contextlib.contextmanager
+    def call(self, what, capture_ok=False):
+        if not self.on_owner_thread():
+            raise RuntimeError(f"{what}: only the thread that built this runner may call it")
+        if self.poisoned or self.shut:
+            raise RuntimeError(f"{what}: this runner is {'poisoned by an earlier failure' if self.poisoned else 'closed'}"
+                               "; build a new one")
+        if torch.cuda.current_stream(self.device).cuda_stream != self.stream.cuda_stream:
+            raise RuntimeError(f"{what}: call on the stream the runner was built on (streams are never switched "
+                               "implicitly)")
+        if not capture_ok:
+            with torch.cuda.device(self.device):
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError(f"{what}: not capturable, it reads a device value back to the host")
+        if not self.busy.acquire(blocking=False):
+            raise RuntimeError(f"{what}: the runner is busy with another call")
+        try:
+            yield
+        except BaseException:
+            self.poisoned = True
+            raise
+        finally:
+            self.busy.release()
+
+    def lease(self, tensors):
+        """Tie ``tensors`` to the runner's stream (record_stream) and hold them until the call
+        that launched work on them has returned."""
+        self.leases = list(tensors)
+        for t in self.leases:
+            t.record_stream(self.stream)
+
+    def release(self):
+        self.leases = []
+
+    def close(self):
+        if not self.on_owner_thread():
+            raise RuntimeError("close: only the thread that built this runner may close it")
+        if self.shut:
+            return
+        if not self.busy.acquire(blocking=False):
+            raise RuntimeError("close: the runner is busy with another call")
+        try:
+            try:
+                self.stream.synchronize()
+            except BaseException:
+                self.poisoned = True          # the leases stay held: the GPU may still use them
+                raise
+            self.drains += 1
+            self.leases = []
+            self.shut = True
+        finally:
+            self.busy.release()
+
+    def state(self):
+        # keys are the reference's lifecycle() report, which callers read
+        return {"failed": self.poisoned, "closed": self.shut, "close_drains": self.drains,
+                "owner_thread_matches": self.on_owner_thread(), "failed_input_leases": len(self.leases),
+                "workspace_owners_retained": True, "caller_weight_pointer_lease_required": True,
+                "raw_addresses_disclosed": False}
+
+
 class CoopRunnerCapacity:
     """Bounded-capacity runner with the ownership rules of CoopRunner3072
-    (runtime/ds41/moe_coop3072.py:261-402). Subclasses fix the default capacity."""
+    (runtime/ds41/moe_coop3072.py:261-402). Subclasses fix the default capacity and whether
+    ``run`` hands back the runner's own output rows (borrowed) or a copy (owned)."""
 
     DEFAULT_MAX_ROWS = 512
+    OWNED_OUTPUT = True
 
     def __init__(self, device="cuda", topk=6, hidden=5120, inter=2304, max_rows=None, *, n_local=None,
                  verbose=False):
@@ -137,12 +222,7 @@ class CoopRunnerCapacity:
         self.topk, self.hidden, self.inter, self.max_rows = topk, hidden, inter, max_rows
         self.n_local = n_local
         self.verbose = verbose
-        self._stream = torch.cuda.current_stream(self.device)
-        self._owner_stream = self._stream.cuda_stream
-        self._owner_thread = threading.get_ident()
-        self._lock, self._failed = threading.Lock(), False
-        self._closed, self._close_drains = False, 0
-        self._failed_inputs = []
+        self._own = _Ownership(self.device)
         self._table_valid = False
         self._ws = {}
         self._last_ws = None
@@ -162,53 +242,41 @@ class CoopRunnerCapacity:
             self._ws[n_local] = ws
         return ws
 
-    def _enter(self, what, allow_capture=False):
-        if threading.get_ident() != self._owner_thread:
-            raise RuntimeError(f"{what} requires the runner's owner thread")
-        if self._failed or self._closed:
-            raise RuntimeError("runner failed or closed; discard it")
-        if torch.cuda.current_stream(self.device).cuda_stream != self._owner_stream:
-            raise RuntimeError(f"{what} requires the construction stream; no implicit cross-stream reuse")
-        if not allow_capture:
-            with torch.cuda.device(self.device):
-                if torch.cuda.is_current_stream_capturing():
-                    raise RuntimeError(f"{what} cannot be captured (it synchronises with the host)")
-        if not self._lock.acquire(blocking=False):
-            raise RuntimeError("runner is already in use")
+    def _check_routes(self, sel, weights, rows):
+        """sel: int64 [rows, topk]; weights: fp16/bf16/fp32 of the same shape; both on the
+        runner's device."""
+        if not isinstance(sel, torch.Tensor) or sel.dtype != torch.int64 or tuple(sel.shape) != (rows, self.topk):
+            raise ValueError(f"sel: expected an int64 tensor of shape ({rows}, {self.topk})")
+        if (not isinstance(weights, torch.Tensor) or weights.shape != sel.shape
+                or weights.dtype not in (torch.float16, torch.bfloat16, torch.float32)):
+            raise ValueError(f"weights: expected a floating tensor (fp16, bf16 or fp32) of shape ({rows}, {self.topk})")
+        if sel.device != self.device or weights.device != self.device:
+            raise ValueError(f"sel and weights must live on {self.device}")
 
-    def _routes(self, x, sel, weights):
+    def _check_x(self, x):
         if (not isinstance(x, torch.Tensor) or x.ndim != 2 or x.shape[1] != self.hidden
                 or not 1 <= x.shape[0] <= self.max_rows or x.dtype not in (torch.float16, torch.bfloat16)):
-            raise ValueError(f"x must be Half/BF16 [1..{self.max_rows},{self.hidden}]")
-        rows = x.shape[0]
-        if (not isinstance(sel, torch.Tensor) or tuple(sel.shape) != (rows, self.topk) or sel.dtype != torch.int64
-                or not isinstance(weights, torch.Tensor) or weights.shape != sel.shape
-                or weights.dtype not in (torch.float16, torch.bfloat16, torch.float32)):
-            raise ValueError(f"routes/weights require [rows,{self.topk}] Long and Half/BF16/Float")
-        if any(t.device != self.device for t in (x, sel, weights)):
-            raise ValueError("inputs must be on the runner device")
-        return rows
+            raise ValueError(f"x: expected an fp16 or bf16 tensor of shape (1..{self.max_rows}, {self.hidden})")
+        if x.device != self.device:
+            raise ValueError(f"x must live on {self.device}")
+        return x.shape[0]
 
     # -- reference API ---------------------------------------------------------------------------
 
     def run(self, x, sel, weights, packed, k, limit, *, check_bounds=True):
-        """Run M rows and return an OWNED fp32 ``[M, hidden]``. Pointer targets are leased by
-        the caller until the GPU is done with them."""
+        """Run M rows; fp32 ``[M, hidden]``, owned or borrowed (``OWNED_OUTPUT``). Pointer
+        targets are leased by the caller until the GPU is done with them."""
         k = _check_rate(k)
         limit = _check_limit(limit)
         if check_bounds not in (True, False):
             raise ValueError("check_bounds must be a bool")
-        rows = self._routes(x, sel, weights)
+        rows = self._check_x(x)
+        self._check_routes(sel, weights, rows)
         table = _pointer_table(packed, self.device, self.n_local)
-        self._enter("run", allow_capture=not check_bounds)
-        try:
-            stream = torch.cuda.current_stream(self.device)
+        with self._own.call("run", capture_ok=not check_bounds):
             x, sel = x.contiguous(), sel.contiguous()
             ws = self._workspace(table.shape[1])
-            inputs = [x, sel, weights, table, ws.buffer, self.out, self.rw]
-            self._failed_inputs = inputs
-            for t in inputs:
-                t.record_stream(stream)
+            self._own.lease([x, sel, weights, table, ws.buffer, self.out, self.rw])
             rw = self.rw[:rows]
             rw.copy_(weights.to(torch.float16))
             ws.clear_flags()
@@ -218,92 +286,52 @@ class CoopRunnerCapacity:
             self._table_valid = True
             if check_bounds and int(ws.flags()[0].item()) != 0:
                 raise RuntimeError("expert index outside the pointer table")
-            output = out.clone()
-            self._failed_inputs = []
-            return output
-        except BaseException:
-            self._failed = True
-            raise
-        finally:
-            self._lock.release()
+            result = out.clone() if self.OWNED_OUTPUT else out
+            self._own.release()
+            return result
 
     def prepare_routes(self, sel, weights, n_local):
         """The run table of these routes (owned int32 ``[2 + 2*max_rows*topk + 1]``)."""
         if type(n_local) is not int or not 1 <= n_local <= 512:
             raise ValueError("n_local must be an integer in 1..512")
-        if (not isinstance(sel, torch.Tensor) or sel.dtype != torch.int64 or sel.ndim != 2
-                or not 1 <= sel.shape[0] <= self.max_rows or sel.shape[1] != self.topk
-                or not isinstance(weights, torch.Tensor) or weights.shape != sel.shape
-                or weights.dtype not in (torch.float16, torch.bfloat16, torch.float32)
-                or sel.device != self.device or weights.device != self.device):
-            raise ValueError("prepare requires same-device bounded Long routes and floating weights")
-        self._enter("prepare_routes")
-        try:
-            stream = torch.cuda.current_stream(self.device)
+        if not isinstance(sel, torch.Tensor) or sel.ndim != 2 or not 1 <= sel.shape[0] <= self.max_rows:
+            raise ValueError(f"sel: expected a 2-D tensor of 1..{self.max_rows} rows")
+        self._check_routes(sel, weights, sel.shape[0])
+        with self._own.call("prepare_routes"):
             sel = sel.contiguous()
+            self._own.lease([sel, weights, self.rw, self.table, self._prep_ws])
             rw = self.rw[:len(sel)]
-            inputs = [sel, weights, self.rw, self.table, self._prep_ws]
-            self._failed_inputs = inputs
-            for t in inputs:
-                t.record_stream(stream)
             rw.copy_(weights.to(torch.float16))
             self._prep_ws[:4].zero_()
             ops.prepare_routes(sel, rw, self.max_rows, n_local, runs=self.table, workspace=self._prep_ws)
             self._last_ws = None
             self._table_valid = True
-            output = self.table.clone()
-            self._failed_inputs = []
-            return output
-        except BaseException:
-            self._failed = True
-            raise
-        finally:
-            self._lock.release()
+            result = self.table.clone()
+            self._own.release()
+            return result
 
     def run_table(self):
         """Owned snapshot of the last run's (or prepare's) table."""
         if not self._table_valid:
-            raise RuntimeError("no table yet")
-        self._enter("run_table")
-        try:
+            raise RuntimeError("run_table: no run or prepare_routes has filled a table yet")
+        with self._own.call("run_table"):
             return (self._last_ws.runs() if self._last_ws is not None else self.table).clone()
-        except BaseException:
-            self._failed = True
-            raise
-        finally:
-            self._lock.release()
 
     def lifecycle(self):
-        """Python ownership state (no device query)."""
-        return dict(failed=self._failed, closed=self._closed, close_drains=self._close_drains,
-                    owner_thread_matches=threading.get_ident() == self._owner_thread,
-                    failed_input_leases=len(self._failed_inputs), workspace_owners_retained=True,
-                    caller_weight_pointer_lease_required=True, raw_addresses_disclosed=False)
+        """Python-side ownership state; queries nothing on the device."""
+        return self._own.state()
 
     def close(self):
-        """Drain the construction stream; a failed drain keeps every lease."""
-        if threading.get_ident() != self._owner_thread:
-            raise RuntimeError("close requires the owner thread")
-        if self._closed:
-            return
-        if not self._lock.acquire(blocking=False):
-            raise RuntimeError("close while the runner is active")
-        try:
-            try:
-                self._stream.synchronize()
-            except BaseException:
-                self._failed = True
-                raise
-            self._close_drains += 1
-            self._failed_inputs = []
-            self._closed = True
-        finally:
-            self._lock.release()
+        """Wait for the construction stream to drain, then refuse further calls. If the drain
+        fails, the runner is poisoned and keeps the tensors of a failed call alive."""
+        self._own.close()
 
 
 class CoopRunner512(CoopRunnerCapacity):
-    """runtime/ds41/moe_coop512.py:170 (default capacity 64 rows)."""
+    """runtime/ds41/moe_coop512.py:170 (default capacity 64 rows). ``run`` returns the runner's
+    own output rows, overwritten by the next call (moe_coop512.py:248)."""
     DEFAULT_MAX_ROWS = 64
+    OWNED_OUTPUT = False
 
 
 class CoopRunner2048(CoopRunnerCapacity):

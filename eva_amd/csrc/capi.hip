@@ -128,7 +128,12 @@ __global__ void fill_i32_kernel(int* p, int n, int v)
     if (i < n) p[i] = v;
 }
 
-static int launched(const char* what)
+void launch_fill_i32(int* p, int n, int v, hipStream_t stream)
+{
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, p, n, v);
+}
+
+int launched(const char* what)
 {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -315,51 +320,68 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
 {
     g_err[0] = 0;
     EVAMX_REQUIRE(a, "evamx_moe_forward: null args");
+    return moe_forward_ws(a, a->workspace, a->workspace_bytes, (hipStream_t)stream, "evamx_moe_forward");
+}
+
+size_t evamx::moe_workspace_bytes_of(const evamx_moe_shape* shape)
+{
+    return shape_ok(shape) ? moe_layout(shape).total : 0;
+}
+
+int evamx::moe_flags_offset(const evamx_moe_shape* shape, size_t* off)
+{
+    if (!shape_ok(shape)) return EVAMX_EINVAL;
+    *off = moe_layout(shape).flags;
+    return EVAMX_OK;
+}
+
+int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                          const char* who)
+{
     const evamx_moe_shape* s = &a->shape;
     if (!shape_ok(s)) return EVAMX_EINVAL;
     const MoeLayout L = moe_layout(s);
-    EVAMX_REQUIRE(a->rows >= 1 && a->rows <= s->rows_max, "evamx_moe_forward: rows %d outside 1..%d", a->rows, s->rows_max);
-    EVAMX_REQUIRE(a->x && (a->out || a->residual) && a->tables && a->sel && a->workspace,
-                  "evamx_moe_forward: null pointer");
-    EVAMX_REQUIRE(a->x_dtype == EVAMX_DTYPE_F16 || a->x_dtype == EVAMX_DTYPE_BF16, "evamx_moe_forward: x_dtype %d", a->x_dtype);
+    EVAMX_REQUIRE(a->rows >= 1 && a->rows <= s->rows_max, "%s: rows %d outside 1..%d", who, a->rows, s->rows_max);
+    EVAMX_REQUIRE(a->x && (a->out || a->residual) && a->tables && a->sel && workspace, "%s: null pointer", who);
+    EVAMX_REQUIRE(a->x_dtype == EVAMX_DTYPE_F16 || a->x_dtype == EVAMX_DTYPE_BF16, "%s: x_dtype %d", who, a->x_dtype);
     EVAMX_REQUIRE(((uintptr_t)a->x & 3) == 0 && a->x_stride % 2 == 0,
-                  "evamx_moe_forward: x must be 4-byte aligned with an even row stride");
+                  "%s: x must be 4-byte aligned with an even row stride", who);
     EVAMX_REQUIRE(a->x_stride >= s->hidden && (!a->out || a->out_stride >= s->hidden) &&
                       (!a->residual || a->residual_stride >= s->hidden),
-                  "evamx_moe_forward: row strides below hidden");
-    EVAMX_REQUIRE(std::isfinite(a->limit) && a->limit >= 0.0f, "evamx_moe_forward: limit must be finite and >= 0");
-    EVAMX_REQUIRE(!(a->logits && a->gate_w), "evamx_moe_forward: give logits or gate_w, not both");
-    EVAMX_REQUIRE(((uintptr_t)a->gate_w & 15) == 0, "evamx_moe_forward: gate_w must be 16-byte aligned");
+                  "%s: row strides below hidden", who);
+    EVAMX_REQUIRE(std::isfinite(a->limit) && a->limit >= 0.0f, "%s: limit must be finite and >= 0", who);
+    EVAMX_REQUIRE(!(a->logits && a->gate_w), "%s: give logits or gate_w, not both", who);
+    EVAMX_REQUIRE(((uintptr_t)a->gate_w & 15) == 0, "%s: gate_w must be 16-byte aligned", who);
     if (a->logits || a->gate_w) {
         EVAMX_REQUIRE(a->n_logits >= s->topk && a->n_logits <= EVAMX_MAX_EXPERTS,
-                      "evamx_moe_forward: n_logits %d must be in topk..%d", a->n_logits, EVAMX_MAX_EXPERTS);
-        EVAMX_REQUIRE(a->weights, "evamx_moe_forward: routing needs a weights output");
+                      "%s: n_logits %d must be in topk..%d", who, a->n_logits, EVAMX_MAX_EXPERTS);
+        EVAMX_REQUIRE(a->weights, "%s: routing needs a weights output", who);
         EVAMX_REQUIRE(a->score_fn == EVAMX_SCORE_SIGMOID || a->score_fn == EVAMX_SCORE_SQRT_SOFTPLUS,
-                      "evamx_moe_forward: unknown score function %d", a->score_fn);
-        EVAMX_REQUIRE(std::isfinite(a->route_scale), "evamx_moe_forward: route_scale must be finite");
+                      "%s: unknown score function %d", who, a->score_fn);
+        EVAMX_REQUIRE(std::isfinite(a->route_scale), "%s: route_scale must be finite", who);
     } else {
-        EVAMX_REQUIRE(a->weights || a->rw_fp16, "evamx_moe_forward: routes need fp32 weights or fp16 rw");
+        EVAMX_REQUIRE(a->weights || a->rw_fp16, "%s: routes need fp32 weights or fp16 rw", who);
     }
     if (a->min_expert >= 0)
-        EVAMX_REQUIRE(a->max_expert > a->min_expert, "evamx_moe_forward: empty expert range");
+        EVAMX_REQUIRE(a->max_expert > a->min_expert, "%s: empty expert range", who);
     int k2u = 0;
     if (!a->k2_per_expert) {
         k2u = rate_k2(a->bits);
-        EVAMX_REQUIRE(gemv_rate(k2u), "evamx_moe_forward: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)a->bits);
+        EVAMX_REQUIRE(gemv_rate(k2u), "%s: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", who, (double)a->bits);
     }
     int k2s = 0;
     if (s->has_shared) {
-        EVAMX_REQUIRE(a->shared, "evamx_moe_forward: shape has a shared expert but no pointers were given");
-        for (int i = 0; i < 9; ++i) EVAMX_REQUIRE(a->shared[i] != 0, "evamx_moe_forward: shared pointer %d is null", i);
+        EVAMX_REQUIRE(a->shared, "%s: shape has a shared expert but no pointers were given", who);
+        for (int i = 0; i < 9; ++i) EVAMX_REQUIRE(a->shared[i] != 0, "%s: shared pointer %d is null", who, i);
         k2s = rate_k2(a->shared_bits);
-        EVAMX_REQUIRE(gemv_rate(k2s), "evamx_moe_forward: shared bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)a->shared_bits);
+        EVAMX_REQUIRE(gemv_rate(k2s), "%s: shared bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", who, (double)a->shared_bits);
     }
-    if (a->workspace_bytes < L.total) {
-        set_error("evamx_moe_forward: workspace %zu bytes < %zu", a->workspace_bytes, L.total);
+    if (workspace_bytes < L.total) {
+        set_error("%s: workspace %zu bytes < %zu", who, workspace_bytes, L.total);
         return EVAMX_ENOSPACE;
     }
 
-    char* ws = (char*)a->workspace;
+    char* ws = (char*)workspace;
     MoeParams p;
     memset(&p, 0, sizeof p);
     p.mode = PREP_GROUP | PREP_MOE;
@@ -405,8 +427,8 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
     p.gemv_waves = gemv_waves();
     p.out = a->out; p.out_stride = a->out_stride;
     p.residual = (uint16_t*)a->residual; p.residual_stride = a->residual_stride;
-    moe_launch(p, (hipStream_t)stream, a->events);
-    return launched("moe_forward");
+    moe_launch(p, stream, a->events);
+    return launched(who);
 }
 
 extern "C" int evamx_bench_decode(float bits, int waves, int iters, float* sink, evamx_stream_t stream)

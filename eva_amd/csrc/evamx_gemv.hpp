@@ -215,7 +215,7 @@ struct GlobalRows {
 // Decode GEMV over one wave's k-range [16*kt0, 16*kt1): acc[m][h] = sum_k X[m][k] * h_k,
 // h_k = 1024 + bytesum of the weight at (k, col(lane, h)) (see mul1_hpair).
 
-// Weight prefetch depth (k-slices in flight per wave). Four slices (8 KiB per wave at 4 bpw)
+// Weight prefetch depth (k-slices in flight per wave). Four slices (4 KiB per wave at 4 bpw)
 // measured best for every chunk width once the waves of a SIMD progress together (depths 4..10
 // at 1 and 2 rows: 4 and 5 the fastest, 10 4% slower).
 template <int TM>

@@ -3,9 +3,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/evamx.h"
+
 namespace evamx {
 
 void set_error(const char* fmt, ...);
+
+// The MoE forward of evamx_moe_forward on a given workspace (validation included); `who` names
+// the entry point in error messages.
+int moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                   const char* who);
+size_t moe_workspace_bytes_of(const evamx_moe_shape* shape);
+int moe_flags_offset(const evamx_moe_shape* shape, size_t* off);
+// n ints at p set to v by a kernel on `stream` (capture-safe, unlike a memset node)
+void launch_fill_i32(int* p, int n, int v, hipStream_t stream);
+// EVAMX_OK, or EVAMX_ELAUNCH with the message set if the last launch failed
+int launched(const char* what);
 
 int launch_dequant(const void* trellis, int in, int out, int k2, void* w, bool scalar, hipStream_t stream);
 

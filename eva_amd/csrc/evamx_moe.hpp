@@ -12,6 +12,7 @@ constexpr int EVAMX_MAX_EXPERTS = 512;     // pointer-table entries per layer (r
 constexpr int EVAMX_MAX_TOPK = 32;         // reference bound: top_k <= 32 (exl3_moe_coop_kernel.cuh:46)
 constexpr int EVAMX_CHUNK = 8;             // slots of one expert per GEMV work item
 constexpr int EVAMX_TILE_ROWS = 64;        // slots of one expert per MFMA work item
+constexpr int EVAMX_SMALL_TILE_ROWS = 16;  // the same for calls of at most 16 tokens (16-row kernel)
 constexpr int EVAMX_MFMA_MIN_ROWS = 3;     // calls with at least this many rows take the MFMA path
                                            // (one decode per tile beats per-row dot2 from 3 rows)
 

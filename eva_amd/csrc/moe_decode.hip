@@ -93,12 +93,6 @@ __device__ __forceinline__ uint16_t bf16_bits(float f)
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-__device__ __forceinline__ half_t load_x16(const void* x, int dtype, size_t i)
-{
-    if (dtype == EVAMX_DTYPE_F16) return ((const half_t*)x)[i];
-    const uint16_t b = ((const uint16_t*)x)[i];
-    return (half_t)__builtin_bit_cast(float, (uint32_t)b << 16);
-}
 
 // ---------------------------------------------------------------------------------------------
 // Router front: logits[r][e] = sum_k float(x[r][k]) * gate_w[e][k] in fp32 (Block.route's
@@ -109,11 +103,18 @@ __device__ __forceinline__ half_t load_x16(const void* x, int dtype, size_t i)
 
 constexpr int GATE_ROWS = 8;
 
+// x as the fp16 value the reference routes and runs the experts on: Block.experts casts the
+// activations to fp16 first (model.py:455), so a bf16 x is rounded to fp16 (values beyond the
+// fp16 range become inf, the fp16 subnormal range keeps fp16 precision).
+__device__ __forceinline__ float x_fp16_value(uint16_t b, int dtype)
+{
+    if (dtype == EVAMX_DTYPE_F16) return h2f(__builtin_bit_cast(half_t, b));
+    return h2f(f2h(__builtin_bit_cast(float, (uint32_t)b << 16)));
+}
+
 __device__ __forceinline__ float x_at(const MoeParams& p, int r, int k)
 {
-    const uint16_t b = ((const uint16_t*)p.x)[(size_t)r * p.x_stride + k];
-    if (p.x_dtype == EVAMX_DTYPE_F16) return h2f(__builtin_bit_cast(half_t, b));
-    return __builtin_bit_cast(float, (uint32_t)b << 16);
+    return x_fp16_value(((const uint16_t*)p.x)[(size_t)r * p.x_stride + k], p.x_dtype);
 }
 
 __global__ __launch_bounds__(256) void moe_gate_kernel(MoeParams p, float* logits)
@@ -321,10 +322,12 @@ __device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lane)
         v[1][i] = (n + 7) >> 3;
         v[2][i] = (n + (1 << cs) - 1) >> cs;
         v[3][i] = p.mfma ? v[2][i] : expert_units(n);          // MFMA tiles are one unit each
-        // MFMA tiles by size: full tiles and a remainder of more than 16 rows are large
+        // MFMA tiles by size: at most 16 rows (small) or more (large); with tiles of at most 16
+        // rows every tile is small, with 64-row tiles the full ones and a remainder of more
+        // than 16 rows are large
         const int rest = n & ((1 << cs) - 1);
-        v[4][i] = p.mfma && rest > 0 && rest <= 16 ? 1 : 0;
-        v[5][i] = p.mfma ? (n >> cs) + (rest > 16 ? 1 : 0) : 0;
+        v[4][i] = !p.mfma ? 0 : cs <= 4 ? v[2][i] : (rest > 0 && rest <= 16 ? 1 : 0);
+        v[5][i] = !p.mfma || cs <= 4 ? 0 : (n >> cs) + (rest > 16 ? 1 : 0);
 #pragma unroll
         for (int k = 0; k < 6; ++k) tot[k] += v[k][i];
     }
@@ -505,7 +508,8 @@ __device__ void group_slots_par(const MoeParams& p, const SelT* sel, const half_
 // grouped slot order.
 // MFMA mode: files tile ci under its size class, in chunk (expert) order within each class: the
 // tiles of at most 16 rows from the front of p.tiles, the larger ones from the back. si / li
-// are the tile's index within its class.
+// are the tile's index within its class (with 64-row tiles an expert has at most one small
+// tile, its last; with 16-row tiles all of its tiles are small).
 __device__ __forceinline__ void file_tile(const MoeParams& p, int ci, int rows, int si, int li)
 {
     if (rows <= 16) p.tiles[si] = ci;
@@ -539,7 +543,7 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             if (!p.mfma)                 // MFMA tiles weigh 1: filled in parallel below
                 for (int i = 0; i < rows; ++i) p.slot_mult[order[c[1] + i]] = m;
             else
-                file_tile(p, ci, rows, ex.small_base[e], ex.large_base[e] + j);   // a small tile is the last
+                file_tile(p, ci, rows, ex.small_base[e] + (CR <= 16 ? j : 0), ex.large_base[e] + j);
             u += m;
         }
     }
@@ -563,15 +567,16 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
             if (!p.mfma)
                 for (int i = 0; i < rows; ++i) p.slot_mult[slots + j * CR + i] = m;
-            else                         // shared tiles follow the routed ones; only the last can be small
-                file_tile(p, base + j, rows, ex.small_base[E], ex.large_base[E] + j);
+            else                         // shared tiles follow the routed ones
+                file_tile(p, base + j, rows, ex.small_base[E] + (CR <= 16 ? j : 0), ex.large_base[E] + j);
         }
     }
     if (p.mfma) {
         for (int s = t; s < moe_nslot(p); s += nt) p.slot_mult[s] = 1;
         if (t == 0) {
             const int sh_rest = p.has_shared ? p.T % CR : 0;
-            p.meta[3] = ex.small_base[E] + (sh_rest > 0 && sh_rest <= 16 ? 1 : 0);
+            const int sh_tiles = p.has_shared ? (p.T + CR - 1) / CR : 0;
+            p.meta[3] = ex.small_base[E] + (CR <= 16 ? sh_tiles : (sh_rest > 0 && sh_rest <= 16 ? 1 : 0));
         }
     }
 }
@@ -598,11 +603,7 @@ constexpr int ROT_BATCH = 8;
 
 __device__ __forceinline__ float x_elem(uint32_t w, int hi, int dtype)
 {
-    if (dtype == EVAMX_DTYPE_F16) {
-        const half2_t h = __builtin_bit_cast(half2_t, w);
-        return h2f(hi ? h.y : h.x);
-    }
-    return __builtin_bit_cast(float, hi ? (w & 0xffff0000u) : (w << 16));
+    return x_fp16_value((uint16_t)(hi ? w >> 16 : w), dtype);
 }
 
 // Chunks [c0, c1) of grouped slot s (routed slot < T*topk with local expert e, or shared row).
@@ -635,8 +636,8 @@ __device__ void rotate_chunks(const MoeParams& p, int s, int e, int proj, int c0
                 if (shared) {
                     // shared EXL3 linear: fp16 product (hadamard_inner.cuh:109-115); routed
                     // experts: fp32 product (exl3_moe_coop_kernel.cuh:186-191)
-                    v0 = h2f(f2h(h2f(f2h(x_elem(xv[j], 0, p.x_dtype))) * h2f(su.x)));
-                    v1 = h2f(f2h(h2f(f2h(x_elem(xv[j], 1, p.x_dtype))) * h2f(su.y)));
+                    v0 = h2f(f2h(x_elem(xv[j], 0, p.x_dtype) * h2f(su.x)));
+                    v1 = h2f(f2h(x_elem(xv[j], 1, p.x_dtype) * h2f(su.y)));
                 }
                 had128_pair(v0, v1, lane);
                 const half2_t r = {f2h(v0), f2h(v1)};
@@ -928,8 +929,9 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
                 float gv = h2f(f2h(h2f(f2h(gg[h])) * gs[c][h]));
                 float uv = h2f(f2h(h2f(f2h(uu[h])) * us[c][h]));
                 if (L > 0.0f) {
-                    uv = fminf(fmaxf(uv, -L), L);
-                    gv = fminf(gv, L);
+                    // torch.clamp: a NaN stays NaN (fminf/fmaxf would return the limit)
+                    uv = uv < -L ? -L : (uv > L ? L : uv);
+                    gv = gv > L ? L : gv;
                 }
                 const float mid = h2f(f2h(silu_f(gv) * uv));
                 av[h] = h2f(f2h(mid * ds[c][h]));
@@ -938,6 +940,7 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
                 float uv = uu[h] * us[c][h];
                 float x = silu_f(gv);
                 if (L != 0.0f) {
+                    // fminf/fmaxf as the reference kernel: a NaN operand yields the limit
                     uv = fminf(fmaxf(uv, -L), L);
                     x = fminf(x, L);
                 }
@@ -1197,7 +1200,9 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     const int nslot = p.T * p.topk + (p.has_shared ? p.T : 0);
     const bool small = moe_small_path(p.T, p.topk);
     p.mfma = p.T >= EVAMX_MFMA_MIN_ROWS ? 1 : 0;
-    p.chunk_rows = p.mfma ? EVAMX_TILE_ROWS : EVAMX_CHUNK;
+    // up to 16 tokens only the 16-row MFMA kernel runs, so the tiles are cut at 16 rows (more
+    // than 16 slots of one expert occur only when given routes repeat an expert within a token)
+    p.chunk_rows = !p.mfma ? EVAMX_CHUNK : p.T <= EVAMX_SMALL_TILE_ROWS ? EVAMX_SMALL_TILE_ROWS : EVAMX_TILE_ROWS;
     hipEvent_t first = ev(0);
     if (p.gate_w) {
         const int waves = p.n_logits * ((p.T + GATE_ROWS - 1) / GATE_ROWS);

@@ -204,10 +204,9 @@ __device__ __forceinline__ int xcd_item_block(int b, int nb)
 // kernels sum the same partials. MBMAX bounds the tile rows in 16-row blocks: the MBMAX 1 kernel
 // (a quarter of the accumulators, 3 waves per SIMD) runs the tiles of at most 16 rows, the
 // MBMAX 4 kernel the larger ones; the split count is the same for both (from all the tiles).
-template <int MBMAX>
-__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(MBMAX == 1 ? 3 : 2))) void moe_mfma_kernel(MoeParams p, int which)
+template <int MBMAX, int which>
+__device__ __forceinline__ void mfma_stage(const MoeParams& p, uint32_t (&lds)[MF_WAVES][MF_LDS_WORDS])
 {
-    __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
     const int wave = threadIdx.x >> 6;
     const int n_all = __builtin_amdgcn_readfirstlane(p.meta[0]);
     const int n_small = __builtin_amdgcn_readfirstlane(p.meta[3]);
@@ -218,7 +217,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(M
     // this launch's tiles: the small ones (at most 16 rows) in the MBMAX 1 kernel when they fill
     // at least three of its resident rounds (3 waves per SIMD), so that its last round's tail is
     // short; the rest (or all) in the MBMAX 4 kernel. Up to 16 tokens every tile is small.
-    const bool split = p.T <= 16 || (long)n_small * per_tile >= 3L * (p.gemv_waves * 3 / 4);
+    const bool split = p.T <= EVAMX_SMALL_TILE_ROWS || (long)n_small * per_tile >= 3L * (p.gemv_waves * 3 / 4);
     const int n_tiles = MBMAX == 1 ? (split ? n_small : 0) : (split ? n_all - n_small : n_all);
     // the call's items fill the first n_blk workgroups (a multiple of 8, spread over the XCDs)
     const int n_blk = ((n_tiles * per_tile + MF_WAVES - 1) / MF_WAVES + 7) & ~7;
@@ -286,6 +285,22 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(M
     }
 }
 
+// The two projection stages as kernels of their own names, so that kernel traces and counter
+// runs tell them apart whatever their grids.
+template <int MBMAX>
+__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(MBMAX == 1 ? 3 : 2))) void moe_gate_up_mfma_kernel(MoeParams p)
+{
+    __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
+    mfma_stage<MBMAX, 0>(p, lds);
+}
+
+template <int MBMAX>
+__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(MBMAX == 1 ? 3 : 2))) void moe_down_mfma_kernel(MoeParams p)
+{
+    __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
+    mfma_stage<MBMAX, 1>(p, lds);
+}
+
 // Launch of one projection stage: enough workgroups for the largest possible item count (the
 // workspace's tile bound times the largest split); workgroups past the call's items exit at once.
 int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
@@ -309,13 +324,16 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     const int s_max = kreq > 0 ? kreq : (cap_rows / nslot < kmax ? (cap_rows / nslot > 1 ? cap_rows / nslot : 1) : kmax);
     const long max_small = (long)(p.n_local < p.T * p.topk ? p.n_local : p.T * p.topk) + (p.has_shared ? 1 : 0);
     const bool may_split = max_small * per_tile * s_max >= 3L * (p.gemv_waves * 3 / 4);
-    if (p.T <= 16) {
-        launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
+    auto k16 = which == 0 ? moe_gate_up_mfma_kernel<1> : moe_down_mfma_kernel<1>;
+    auto k64 = which == 0 ? moe_gate_up_mfma_kernel<4> : moe_down_mfma_kernel<4>;
+    const dim3 grid((unsigned)blocks), block(64 * MF_WAVES);
+    if (p.T <= EVAMX_SMALL_TILE_ROWS) {
+        launch_timed(k16, grid, block, stream, start, stop, p);
     } else if (!may_split) {
-        launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, stop, p, which);
+        launch_timed(k64, grid, block, stream, start, stop, p);
     } else {
-        launch_timed(moe_mfma_kernel<1>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, start, nullptr, p, which);
-        launch_timed(moe_mfma_kernel<4>, dim3((unsigned)blocks), dim3(64 * MF_WAVES), stream, nullptr, stop, p, which);
+        launch_timed(k16, grid, block, stream, start, nullptr, p);
+        launch_timed(k64, grid, block, stream, nullptr, stop, p);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

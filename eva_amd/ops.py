@@ -186,58 +186,94 @@ class MoeWorkspace:
         return self.buffer[off:off + 4].view(torch.int32)
 
 
-def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: torch.Tensor | None, *, limit: float,
-                bits: float | None = None, k2_per_expert: torch.Tensor | None = None,
-                logits: torch.Tensor | None = None, sel: torch.Tensor | None = None,
-                weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
-                score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
-                shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0,
-                events=None, residual: torch.Tensor | None = None, gate_w: torch.Tensor | None = None):
-    """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
+def _check_forward_args(s, device, x, tables, out, bits, k2_per_expert, logits, sel, weights, rw, sel_bias,
+                        shared_ptrs, shared_bits, events, residual, gate_w):
+    """Every tensor's device, dtype and shape against the workspace's shape, before any launch:
+    the C ABI receives bare pointers and would read or write out of bounds otherwise."""
+    def on_dev(t, name, dtype, shape=None, row_strided=False):
+        _dev(t, name, dtype, len(shape) if shape is not None else None, row_strided=row_strided)
+        if t.device != device:
+            raise ValueError(f"{name} is on {t.device}, the workspace on {device}")
+        if shape is not None:
+            for i, (have, want) in enumerate(zip(t.shape, shape)):
+                if want is not None and have != want:
+                    raise ValueError(f"{name} must have shape {tuple('*' if w is None else w for w in shape)}, "
+                                     f"got {tuple(t.shape)}")
 
-    With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
-    must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
-    the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
-    ``events``: optional ctypes array of 10 hipEvent_t handles: start and end timestamps of the
-    5 stages' kernels (prepare, gate/up, activation, down, combine).
-    ``residual``: optional bf16 ``[rows, H]`` stream updated in place to ``bf16(residual + bf16(y))``
-    (may be ``x`` itself); ``out`` may then be None.
-    ``gate_w``: optional fp32 ``[n_experts, H]`` router weight; the logits ``x @ gate_w.T`` are then
-    computed on the device (instead of ``logits``) and routed with ``score_fn``/``sel_bias``.
-    """
-    s = ws.shape
-    _dev(x, "x", None, 2, row_strided=True)
+    on_dev(x, "x", None, (None, s.hidden), row_strided=True)
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("x must be fp16 or bf16")
-    _dev(tables, "tables", torch.int64, 2)
+    rows, topk = x.shape[0], s.topk
+    if not 1 <= rows <= s.rows_max:
+        raise ValueError(f"x has {rows} rows, the workspace holds 1..{s.rows_max}")
+    on_dev(tables, "tables", torch.int64, (9, s.n_local))
     if out is None and residual is None:
         raise ValueError("need out, residual or both")
     if out is not None:
-        _dev(out, "out", torch.float32, 2, row_strided=True)
+        on_dev(out, "out", torch.float32, (None, None), row_strided=True)
+        if out.shape[0] < rows or out.shape[1] < s.hidden:
+            raise ValueError(f"out must be at least [{rows}, {s.hidden}], got {tuple(out.shape)}")
     if residual is not None:
-        _dev(residual, "residual", torch.bfloat16, 2, row_strided=True)
-        if residual.shape[0] != x.shape[0] or residual.shape[1] < s.hidden:
-            raise ValueError("residual must be [rows, >= hidden]")
-    if tables.shape != (9, s.n_local):
-        raise ValueError(f"tables must be [9, {s.n_local}]")
-    rows = x.shape[0]
+        on_dev(residual, "residual", torch.bfloat16, (rows, None), row_strided=True)
+        if residual.shape[1] < s.hidden:
+            raise ValueError(f"residual must be [{rows}, >= {s.hidden}]")
+    if sel is None:
+        raise ValueError("sel is required (routes in, or the routing's output)")
+    on_dev(sel, "sel", torch.int64, (rows, topk))
+    if weights is not None:
+        on_dev(weights, "weights", torch.float32, (rows, topk))
+    if rw is not None:
+        on_dev(rw, "rw", torch.float16, (rows, topk))
+    if logits is not None and gate_w is not None:
+        raise ValueError("give logits or gate_w, not both")
+    routing = logits is not None or gate_w is not None
+    if routing:
+        if weights is None:
+            raise ValueError("routing on the device writes weights: pass an fp32 [rows, topk] output")
+        if logits is not None:
+            on_dev(logits, "logits", torch.float32, (rows, None))
+            n_logits = logits.shape[1]
+        else:
+            on_dev(gate_w, "gate_w", torch.float32, (None, s.hidden))
+            n_logits = gate_w.shape[0]
+        if not topk <= n_logits <= 512:
+            raise ValueError(f"{n_logits} experts in the router, need {topk}..512")
+        if sel_bias is not None:
+            on_dev(sel_bias, "sel_bias", torch.float32, (n_logits,))
+    elif weights is None and rw is None:
+        raise ValueError("given routes need fp32 weights or fp16 rw")
+    elif sel_bias is not None:
+        raise ValueError("sel_bias applies only when routing on the device")
+    if k2_per_expert is not None:
+        on_dev(k2_per_expert, "k2_per_expert", torch.uint8, (s.n_local,))
+    elif bits is None:
+        raise ValueError("give a uniform rate (bits) or k2_per_expert")
+    if s.has_shared:
+        if shared_ptrs is None or len(shared_ptrs) != 9 or shared_bits is None:
+            raise ValueError("the workspace has a shared expert: pass its 9 pointers and shared_bits")
+    elif shared_ptrs is not None:
+        raise ValueError("the workspace was built without a shared expert")
+    if events is not None and len(events) != 10:
+        raise ValueError("events must hold 10 event handles")
+
+
+def _moe_args(s, device, x, tables, out, limit, bits, k2_per_expert, logits, sel, weights, rw, score_fn, sel_bias,
+              route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events, residual, gate_w):
+    """The evamx_moe_args of one forward call (every tensor checked first), without the
+    workspace; returns it with the ctypes array of shared pointers it refers to."""
+    _check_forward_args(s, device, x, tables, out, bits, k2_per_expert, logits, sel, weights, rw, sel_bias,
+                        shared_ptrs, shared_bits, events, residual, gate_w)
     a = MoeArgs()
     a.shape = s
-    a.rows = rows
+    a.rows = x.shape[0]
     a.x = ptr(x)
     a.x_dtype = _lib.DTYPE_F16 if x.dtype == torch.float16 else _lib.DTYPE_BF16
     a.x_stride = x.stride(0)
-    if logits is not None and gate_w is not None:
-        raise ValueError("give logits or gate_w, not both")
     if logits is not None or gate_w is not None:
         if logits is not None:
-            _dev(logits, "logits", torch.float32, 2)
             a.logits = ptr(logits)
             a.n_logits = logits.shape[1]
         else:
-            _dev(gate_w, "gate_w", torch.float32, 2)
-            if gate_w.shape[1] != s.hidden:
-                raise ValueError(f"gate_w must be [n_experts, {s.hidden}]")
             a.gate_w = ptr(gate_w)
             a.n_logits = gate_w.shape[0]
         a.sel_bias = ptr(sel_bias)
@@ -262,10 +298,35 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     if residual is not None:
         a.residual = ptr(residual)
         a.residual_stride = residual.stride(0)
-    a.workspace = ptr(ws.buffer)
-    a.workspace_bytes = ws.buffer.numel()
     if events is not None:
         a.events = ctypes.cast(events, ctypes.c_void_p)
+    return a, keep
+
+
+def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: torch.Tensor | None, *, limit: float,
+                bits: float | None = None, k2_per_expert: torch.Tensor | None = None,
+                logits: torch.Tensor | None = None, sel: torch.Tensor | None = None,
+                weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
+                score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
+                shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0,
+                events=None, residual: torch.Tensor | None = None, gate_w: torch.Tensor | None = None):
+    """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
+
+    With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
+    must be given as outputs); otherwise ``sel`` with ``weights`` (fp32) or ``rw`` (fp16) are
+    the routes. ``tables``: int64 ``[9, n_local]`` device pointer table. ``shared_ptrs``: 9 ints.
+    ``events``: optional ctypes array of 10 hipEvent_t handles: start and end timestamps of the
+    5 stages' kernels (prepare, gate/up, activation, down, combine).
+    ``residual``: optional bf16 ``[rows, H]`` stream updated in place to ``bf16(residual + bf16(y))``
+    (may be ``x`` itself); ``out`` may then be None.
+    ``gate_w``: optional fp32 ``[n_experts, H]`` router weight; the logits ``x @ gate_w.T`` are then
+    computed on the device (instead of ``logits``) and routed with ``score_fn``/``sel_bias``.
+    """
+    a, keep = _moe_args(ws.shape, ws.buffer.device, x, tables, out, limit, bits, k2_per_expert, logits, sel, weights,
+                        rw, score_fn, sel_bias, route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events,
+                        residual, gate_w)
+    a.workspace = ptr(ws.buffer)
+    a.workspace_bytes = ws.buffer.numel()
     check(lib().evamx_moe_forward(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward")
     del keep
     return out

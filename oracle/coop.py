@@ -258,12 +258,13 @@ def silu_f32(g):
 
 
 def act_gate(g, u, limit):
-    """K.cuh:115-129 (SiLU, gated): ``min(silu(g), L) * clamp(u, -L, L)`` when L != 0."""
+    """K.cuh:115-129 (SiLU, gated): ``min(silu(g), L) * clamp(u, -L, L)`` when L != 0, with the
+    kernel's fminf/fmaxf, which return the other operand when one is NaN (np.fmin/np.fmax)."""
     x = silu_f32(g)
     u = _f32(u)
     if limit != 0:
-        u = np.clip(u, F32(-limit), F32(limit)).astype(np.float32)
-        x = np.minimum(x, F32(limit)).astype(np.float32)
+        u = np.fmin(np.fmax(u, F32(-limit)), F32(limit)).astype(np.float32)
+        x = np.fmin(x, F32(limit)).astype(np.float32)
     return (x * u).astype(np.float32)
 
 
@@ -328,7 +329,8 @@ def exl3_linear(x_fp16, trellis, suh, svh, K, W=None):
 
 
 def swiglu(gate, up, limit):
-    """kernels.py:213-217: clamp the gate from above BEFORE SiLU, the up symmetrically."""
+    """kernels.py:213-217: clamp the gate from above BEFORE SiLU, the up symmetrically, with
+    torch.clamp's semantics (a NaN stays NaN: np.clip / np.minimum)."""
     gate = _f32(gate)
     up = _f32(up)
     if limit > 0:

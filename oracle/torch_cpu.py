@@ -95,19 +95,29 @@ def expert_forward(x: torch.Tensor, parts, dec: Decoder, limit: float, shared: b
     return rotate(ar @ dec.dequant(tr)) * svh.float()
 
 
-def moe_layer(x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, experts, shared, dec: Decoder, limit: float):
-    """Routed slots in slot order plus the shared expert; x fp32 [T, H]."""
+def route_sigmoid(logits: torch.Tensor, topk: int, route_scale: float = 1.0):
+    """Block.route with sigmoid scores (model.py:404-416 with the DeepSeek-V3 score): top-k of
+    the logits (sigmoid is monotone), weights normalised over the picks and scaled."""
+    z, idx = torch.topk(logits, topk, dim=-1)
+    s = torch.sigmoid(z)
+    return idx, s / (s.sum(-1, keepdim=True) + 1e-20) * route_scale
+
+
+def moe_layer(x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, experts, shared, dec, limit: float):
+    """Routed slots in slot order plus the shared expert; x fp32 [T, H]. ``dec``: one Decoder for
+    every expert, or a dict of Decoders by expert index with the shared expert's under -1."""
+    dec_of = (lambda e: dec[e]) if isinstance(dec, dict) else (lambda e: dec)
     t, k = idx.shape
     out = torch.zeros_like(x)
     cache = {}
     for e in sorted(set(idx.reshape(-1).tolist())):
         rows = [r for r in range(t) if e in idx[r].tolist()]
-        cache[e] = (rows, expert_forward(x[rows], experts[e], dec, limit, False))
+        cache[e] = (rows, expert_forward(x[rows], experts[e], dec_of(e), limit, False))
     for r in range(t):
         for j in range(k):
             e = int(idx[r, j])
             rows, o = cache[e]
             out[r] += w[r, j] * o[rows.index(r)]
     if shared is not None:
-        out += expert_forward(x, shared, dec, limit, True)
+        out += expert_forward(x, shared, dec_of(-1), limit, True)
     return out

@@ -41,3 +41,24 @@ def rel_err_rows(y, ref):
     y = np.asarray(y, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     return float((np.abs(y - ref).max(axis=-1) / np.maximum(np.abs(ref).max(axis=-1), 1e-30)).max())
+
+
+def clamp_variants(compute):
+    """``compute()`` under the oracle's activation semantics and three wrong ones, to give a
+    test of the SwiGLU limit teeth: the reference clamps a routed expert's gate AFTER SiLU
+    (exl3_moe_coop_kernel.cuh:115-129) and the shared expert's gate BEFORE SiLU
+    (kernels.py:213-217). Returns {"ref", "routed_swapped", "shared_swapped", "unclamped"}."""
+    from oracle import coop
+
+    act, sw = coop.act_gate, coop.swiglu
+    out = {"ref": compute()}
+    variants = {"routed_swapped": (lambda g, u, L: sw(g, u, L), sw),
+                "shared_swapped": (act, lambda g, u, L: act(g, u, L)),
+                "unclamped": (lambda g, u, L: act(g, u, 0.0), lambda g, u, L: sw(g, u, 0.0))}
+    try:
+        for name, (a, s) in variants.items():
+            coop.act_gate, coop.swiglu = a, s
+            out[name] = compute()
+    finally:
+        coop.act_gate, coop.swiglu = act, sw
+    return out

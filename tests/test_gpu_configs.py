@@ -6,7 +6,8 @@
 - config 4: 512-token prefill with Zipf routing and per-expert rates {2,3,4,5}: the oracle on a
   reduced width, and at the full DSv3 width a batch-invariance property (each row of the
   512-row call equals the same row run alone) plus the oracle on two rows;
-- config 5: stacked layers at 2.5 bpw with the fused bf16 residual, against the oracle's stack.
+- config 5: stacked layers at 2.5 bpw with the fused bf16 residual, against the oracle's stack
+  (3 reduced-width layers eager, and 3 DSv3-width layers captured as one hipGraph).
 Bars: indices bit-exact; outputs within max row-relative error 1e-2.
 """
 import numpy as np
@@ -14,10 +15,11 @@ import pytest
 import torch
 
 from oracle import coop, exl3, synth
-from tests.gpu_helpers import DeviceExperts, rel_err_rows, to_dev
+from tests.gpu_helpers import DeviceExperts, clamp_variants, rel_err_rows, to_dev
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
+CLIP = 0.75          # SwiGLU limit that clips ~12% of SiLU(G) and ~45% of U at these scales
 
 
 def test_config1_linear(dev):
@@ -34,20 +36,24 @@ def test_config1_linear(dev):
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
 
 
-def _moe(ops, dev, H, I, E, topk, rows, experts_dev, k2, x, logits, shared_dev=None, shared_bits=None):
+def _moe(ops, dev, H, I, E, topk, rows, experts_dev, k2, x, logits, shared_dev=None, shared_bits=None, limit=10.0):
     ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E,
                           has_shared=shared_dev is not None)
     sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
     w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
     out = torch.empty(rows, H, dtype=torch.float32, device=dev)
-    ops.moe_forward(ws, x, experts_dev, out, limit=10.0, k2_per_expert=k2, logits=logits, sel=sel, weights=w,
+    ops.moe_forward(ws, x, experts_dev, out, limit=limit, k2_per_expert=k2, logits=logits, sel=sel, weights=w,
                     shared_ptrs=shared_dev, shared_bits=shared_bits)
     torch.cuda.synchronize()
     assert int(ws.flags().cpu()[0]) == 0
     return out, sel
 
 
-def test_config4_prefill_reduced(dev):
+@pytest.mark.parametrize("limit", [10.0, CLIP])
+def test_config4_prefill_reduced(dev, limit):
+    """512 tokens, Zipf routing, rates {2,3,4,5} through the 16- and 64-row MFMA kernels; at CLIP
+    the SwiGLU limit clips in the routed (after SiLU) and the shared (before SiLU) expert, and
+    the result must be far from the layer with either clamp order swapped or no clamp."""
     from eva_amd import ops
     H, I, E, topk, T = 1024, 256, 64, 8, 512
     rng = np.random.default_rng(104)
@@ -56,12 +62,19 @@ def test_config4_prefill_reduced(dev):
     shared = synth.expert(rng, H, I, 4, 1 / np.sqrt(H))
     x = synth.activations_bf16(rng, T, H)
     logits = synth.logits_zipf(rng, T, E)
-    ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, topk, 10.0)
+    compute = lambda: coop.moe_layer(x, logits, experts, shared, topk, limit)[0]
+    variants = clamp_variants(compute) if limit == CLIP else {"ref": compute()}
+    ridx, _ = coop.route(logits, topk)
     de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
     out, sel = _moe(ops, dev, H, I, E, topk, T, de.table, de.k2, to_dev(x, dev).to(torch.bfloat16),
-                    to_dev(logits, dev), ds.ptrs(0), 4.0)
+                    to_dev(logits, dev), ds.ptrs(0), 4.0, limit=limit)
     assert np.array_equal(sel.cpu().numpy(), ridx)
-    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+    y = out.cpu().numpy()
+    assert rel_err_rows(y, variants["ref"]) < TOL
+    if limit == CLIP:
+        for name in ("routed_swapped", "shared_swapped", "unclamped"):
+            assert rel_err_rows(variants[name], variants["ref"]) > 5 * TOL, name
+            assert rel_err_rows(y, variants[name]) > 2 * TOL, name
 
 
 class _DeviceRandomExperts:
@@ -146,3 +159,64 @@ def test_config5_stack_residual(dev):
     # the layers' contribution, allowing one bf16 half-ulp per residual rounding per layer
     bound = L * np.maximum(np.abs(ref), np.abs(got)) * 2.0 ** -8 + TOL * np.abs(ref - h0).max()
     assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_config5_dsv3_width_layers_in_one_graph(dev):
+    """configs[4] at its real width: 3 DSv3-shape layers (H=7168, I=2048, 256 routed + 1 shared,
+    top-8) at 2.5 bpw, 8 tokens, independent seeded routing per layer, each layer adding its
+    output into the bf16 residual stream (model.py:498-499), the whole step captured as ONE
+    hipGraph. Every replay (with eager work in between) must give the same bits as the eager
+    step, and the stream must match the oracle's layer_stack on the touched experts."""
+    from eva_amd import ops
+    H, I, E, topk, T, L, K, limit = 7168, 2048, 256, 8, 8, 3, 2.5, 10.0
+    rng = np.random.default_rng(505)
+    logits = [synth.logits_skewed(rng, T, E, hot=2, warm=6) for _ in range(L)]
+    h0 = synth.activations_bf16(rng, T, H)
+    dummy = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
+    layers, tables, shared_ptrs, keep = [], [], [], []
+    for l in range(L):
+        used = sorted(set(int(v) for v in coop.route(logits[l], topk)[0].reshape(-1)))
+        experts = {e: synth.expert(rng, H, I, K, 1 / np.sqrt(H)) for e in used}
+        shared = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
+        layers.append((experts, shared))
+        de = DeviceExperts([experts[e] for e in used] + [dummy], dev)
+        host = de.table.cpu()
+        cols = {e: i for i, e in enumerate(used)}
+        tables.append(torch.stack([host[:, cols.get(e, len(used))] for e in range(E)], dim=1).contiguous().to(dev))
+        ds = DeviceExperts([shared], dev)
+        shared_ptrs.append(ds.ptrs(0))
+        keep += [de, ds]
+    ref = coop.layer_stack(h0, logits, layers, topk, limit)
+
+    ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    h_in = to_dev(h0, dev).to(torch.bfloat16)
+    h = torch.empty_like(h_in)
+    z = [to_dev(v, dev) for v in logits]
+    sel = torch.empty(L, T, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(L, T, topk, dtype=torch.float32, device=dev)
+
+    def step():
+        h.copy_(h_in)
+        for l in range(L):
+            ops.moe_forward(ws, h, tables[l], None, limit=limit, bits=K, logits=z[l], sel=sel[l], weights=w[l],
+                            shared_ptrs=shared_ptrs[l], shared_bits=K, residual=h)
+
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    eager = h.clone()
+    for l in range(L):
+        assert np.array_equal(sel[l].cpu().numpy(), coop.route(logits[l], topk)[0])
+    assert rel_err_rows(eager.float().cpu().numpy(), ref) < TOL
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    for i in range(3):
+        h.fill_(0)                                         # eager work between the replays
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(h, eager), i

@@ -8,11 +8,21 @@ import pytest
 import torch
 
 from oracle import coop, exl3, synth
-from tests.gpu_helpers import DeviceExperts, rel_err_rows, to_dev
+from tests.gpu_helpers import DeviceExperts, clamp_variants, rel_err_rows, to_dev
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+CLIP = 0.75          # SwiGLU limit that clips ~12% of SiLU(G) and ~45% of U at these scales
+
+
+def _assert_clamp_parity(y, variants):
+    """y matches the reference clamp semantics and none of the wrong ones (the wrong ones sit
+    far outside the tolerance at CLIP, so a kernel that skips or reorders a clamp fails)."""
+    assert rel_err_rows(y, variants["ref"]) < TOL
+    for name in ("routed_swapped", "shared_swapped", "unclamped"):
+        assert rel_err_rows(variants[name], variants["ref"]) > 5 * TOL, name
+        assert rel_err_rows(y, variants[name]) > 2 * TOL, name
 
 
 def _ops():
@@ -93,11 +103,14 @@ def _layer_case(rng, H, I, E, K, svh_scale, rates=None):
     return experts, shared
 
 
+@pytest.mark.parametrize("limit", [10.0, CLIP])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 16])
 @pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
-def test_moe_layer_small(dev, rows, K):
+def test_moe_layer_small(dev, rows, K, limit):
+    """Layer parity through the decode GEMV (1-2 rows) and the MFMA tiles (3+ rows); at CLIP the
+    SwiGLU limit clips and both clamp orders (routed after SiLU, shared before) are checked."""
     ops = _ops()
-    H, I, E, topk, limit = 512, 256, 24, 4, 10.0
+    H, I, E, topk = 512, 256, 24, 4
     rng = np.random.default_rng(int(1000 * rows + 2 * K))
     experts, shared = _layer_case(rng, H, I, E, K, 1 / np.sqrt(H))
     x = synth.activations_bf16(rng, rows, H)
@@ -120,6 +133,8 @@ def test_moe_layer_small(dev, rows, K):
     assert rel_err_rows(y, ref) < TOL
     runs = ws.runs().cpu().numpy()
     assert np.array_equal(runs, coop.reference_table(ridx, rrw, capacity=16))
+    if limit == CLIP:
+        _assert_clamp_parity(y, clamp_variants(lambda: coop.moe_layer(x, logits, experts, shared, topk, limit)[0]))
 
 
 @pytest.mark.parametrize("rows", [1, 2])
@@ -151,9 +166,9 @@ _DSV3_CASES = {}
 
 
 def _dsv3_case(rows):
-    """Seeded DSv3-shape inputs and the oracle output on the touched experts (cached per rows)."""
+    """Seeded DSv3-shape inputs and the touched experts (cached per rows)."""
     if rows not in _DSV3_CASES:
-        H, I, E, topk, limit, K = 7168, 2048, 256, 8, 10.0, 4
+        H, I, E, topk, K = 7168, 2048, 256, 8, 4
         rng = np.random.default_rng(42 + rows)
         x = synth.activations_bf16(rng, rows, H)
         logits = synth.logits_plain(rng, rows, E) if rows == 1 else synth.logits_skewed(rng, rows, E)
@@ -161,20 +176,29 @@ def _dsv3_case(rows):
         used = sorted(set(int(v) for v in ridx.reshape(-1)))
         experts = {e: synth.expert(rng, H, I, K, 1 / np.sqrt(H)) for e in used}
         shared = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
-        ref, _, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
-        _DSV3_CASES[rows] = (x, logits, ridx, used, experts, shared, ref)
+        _DSV3_CASES[rows] = (x, logits, ridx, used, experts, shared, {})
     return _DSV3_CASES[rows]
 
 
+def _dsv3_ref(rows, limit):
+    x, logits, _, _, experts, shared, refs = _dsv3_case(rows)
+    if limit not in refs:
+        compute = lambda: coop.moe_layer(x, logits, experts, shared, 8, limit)[0]
+        refs[limit] = clamp_variants(compute) if limit == CLIP else {"ref": compute()}
+    return refs[limit]
+
+
 @pytest.mark.parametrize("rows", [1, 16])
-@pytest.mark.parametrize("ks", [(0, 0), (32, 16), (3, 5)])
-def test_moe_layer_dsv3_shape(dev, rows, ks):
+@pytest.mark.parametrize("ks,limit", [((0, 0), 10.0), ((32, 16), 10.0), ((3, 5), 10.0), ((0, 0), CLIP)])
+def test_moe_layer_dsv3_shape(dev, rows, ks, limit):
     """DeepSeek-V3 shape (H=7168, I=2048, 256 routed + 1 shared, top-8, 4 bpw), oracle on the
     touched experts only; automatic k-splits, and requested ones above and below the split that
-    fills the GPU once (every split's partials must be written and summed)."""
+    fills the GPU once (every split's partials must be written and summed); at CLIP the SwiGLU
+    limit clips in both the routed and the shared expert."""
     ops = _ops()
-    H, I, E, topk, limit, K = 7168, 2048, 256, 8, 10.0, 4
-    x, logits, ridx, used, experts, shared, ref = _dsv3_case(rows)
+    H, I, E, topk, K = 7168, 2048, 256, 8, 4
+    x, logits, ridx, used, experts, shared, _ = _dsv3_case(rows)
+    variants = _dsv3_ref(rows, limit)
 
     # Device table: touched experts at their indices, a dummy expert everywhere else.
     dummy = synth.expert(np.random.default_rng(0), H, I, K)
@@ -198,7 +222,10 @@ def test_moe_layer_dsv3_shape(dev, rows, ks):
                     logits=to_dev(logits, dev), sel=sel, weights=w, shared_ptrs=ds.ptrs(0), shared_bits=K)
     torch.cuda.synchronize()
     assert np.array_equal(sel.cpu().numpy(), ridx)
-    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+    y = out.cpu().numpy()
+    assert rel_err_rows(y, variants["ref"]) < TOL
+    if limit == CLIP:
+        _assert_clamp_parity(y, variants)
 
 
 @pytest.mark.parametrize("rate_set", [(2, 3, 4, 5), (1.5, 2.5, 3.5, 4)])
@@ -245,6 +272,74 @@ def test_moe_given_routes_repeating_an_expert(dev, rows):
     torch.cuda.synchronize()
     assert int(ws.flags().cpu()[0]) == 0
     assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("rows,pattern", [(3, "all_one"), (16, "hot_twice"), (2, "all_one"), (20, "hot_twice")])
+def test_moe_repeated_expert_fills_many_tiles(dev, rows, pattern):
+    """Given routes repeating an expert inside tokens put more slots on one expert than a 16-row
+    MFMA tile holds: T=3 with all 24 slots on one expert, T=16 with one expert twice in every
+    token (32 slots), against the oracle over a workspace filled with garbage first (a tile
+    whose partials were never written would read it)."""
+    ops = _ops()
+    H, I, E, topk, limit = 256, 256, 6, 8, CLIP
+    rng = np.random.default_rng(400 + rows)
+    experts, shared = _layer_case(rng, H, I, E, 4, 1 / np.sqrt(H))
+    x = rng.standard_normal((rows, H)).astype(np.float16)
+    sel = rng.integers(0, E, size=(rows, topk)).astype(np.int64)
+    if pattern == "all_one":
+        sel[:] = 2
+    else:
+        sel[:, 0] = sel[:, 5] = 4
+    rw = rng.uniform(0.1, 1.0, size=(rows, topk)).astype(np.float16)
+    ref = coop.moe_routed(x, sel, rw, experts, limit)
+    ref = (ref + coop.shared_expert(x, shared, limit)).astype(np.float32)
+    de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    ws.buffer.fill_(0x7f)
+    ws.clear_flags()
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev), de.table, out, limit=limit, bits=4, sel=to_dev(sel, dev),
+                    rw=to_dev(rw, dev), shared_ptrs=ds.ptrs(0), shared_bits=4)
+    torch.cuda.synchronize()
+    assert int(ws.flags().cpu()[0]) == 0
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_moe_bf16_x_rounds_to_fp16(dev, rows):
+    """The reference casts the activations to fp16 before routing and the experts
+    (model.py:455): bf16 values past the fp16 range become inf, and values in the fp16 subnormal
+    range lose precision or flush. Row 0 holds 70000 (inf in fp16: that row's output is all
+    non-finite, as the oracle's); the other rows hold subnormal-range values, including 2e-8,
+    which rounds to zero (their effect on a layer output is below the tolerance; the router
+    test checks their rounding against fp32-tight logits)."""
+    ops = _ops()
+    H, I, E, topk, limit, K = 512, 256, 16, 4, 10.0, 4
+    rng = np.random.default_rng(500 + rows)
+    experts, shared = _layer_case(rng, H, I, E, K, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, rows, H)
+    x[0, 17] = 70000.0
+    tiny = np.array([3.0e-5, -1.1e-6, 2.0e-8, 6.0e-7, -4.4e-5], np.float32)
+    for r in range(1, rows):
+        x[r, 5 * r:5 * r + 5] = tiny
+    x = coop.round_bf16(x)
+    assert np.isinf(x.astype(np.float16)[0, 17]) and (x.astype(np.float16)[1:, :] == 0).sum() >= rows - 1
+    logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
+    ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+    de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), de.table, out, limit=limit, bits=K,
+                    logits=to_dev(logits, dev), sel=sel, weights=w, shared_ptrs=ds.ptrs(0), shared_bits=K)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), ridx)
+    y = out.cpu().numpy()
+    assert not np.isfinite(ref[0]).any() and not np.isfinite(y[0]).any()
+    if rows > 1:
+        assert np.isfinite(y[1:]).all()
+        assert rel_err_rows(y[1:], ref[1:]) < TOL
 
 
 def test_moe_out_of_range_expert_sets_flag(dev):

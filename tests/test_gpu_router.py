@@ -176,3 +176,23 @@ def test_block_route_mirror(dev, rows):
                     gate_w=to_dev(gate_w, dev), sel=sel, weights=wt)
     torch.cuda.synchronize()
     assert np.array_equal(ws.logits(rows, E).cpu().numpy().view(np.uint32), zn.view(np.uint32))
+
+
+def test_router_logits_round_bf16_x_to_fp16(dev):
+    """Block.experts routes on ``x.to(float16)`` (model.py:455, then x.float() @ gate_w at
+    :404-409): bf16 activations are rounded to fp16 first. Row 1 lies in the fp16 subnormal range
+    (about 4 significant bits there), so the rounding moves its logits far outside the fp32
+    accumulation bound; row 2 holds 70000, inf in fp16, so its logits are infinite."""
+    ops = _ops()
+    H, E = 1024, 64
+    rng = np.random.default_rng(12)
+    x = synth.activations_bf16(rng, 3, H)
+    x[1] = coop.round_bf16(x[1] * 2.0e-6)
+    x[2, 100] = 70000.0
+    gate_w = _gate(rng, E, H)
+    z = ops.router_logits(to_dev(x, dev).to(torch.bfloat16), to_dev(gate_w, dev)).cpu().numpy()
+    xh = x.astype(np.float16).astype(np.float32)
+    _check_logits(z[:2], xh[:2], gate_w)
+    with pytest.raises(AssertionError):                  # the unrounded values miss the bound
+        _check_logits(z[1:2], x[1:2], gate_w)
+    assert np.all(np.isinf(z[2])) and np.array_equal(np.sign(z[2]), np.sign(gate_w[:, 100]))

@@ -54,7 +54,7 @@ def test_capacity_runner_run_prepare_table(dev, case):
         w[1, 2] = 0.0
         y = r.run(to_dev(x, dev), to_dev(sel, dev), to_dev(w, dev), de.table, 3, 10.0)
         rw16 = w.astype(np.float16)
-        assert y.shape == (rows, H)
+        assert y.shape == (rows, H) and y.data_ptr() != r.out.data_ptr()   # owned copy (moe_coop3072.py:312)
         assert rel_err_rows(y.cpu().numpy(), coop.moe_routed(x, sel, rw16, ex, 10.0)) < TOL
         assert np.array_equal(r.run_table().cpu().numpy(), coop.reference_table(sel, rw16, capacity=20))
         t = r.prepare_routes(to_dev(sel, dev), to_dev(w, dev), E)
@@ -83,6 +83,8 @@ def test_capacity_runner_bounds_poison_and_owner(dev, case):
     assert errors                                              # wrong thread refused
     with pytest.raises(ValueError):
         r.run(x, good, w, de.table, 6, 1.0)                    # unsupported rate: argument error
+    y1 = r.run(x, good, w, de.table, 3, 1.0)
+    assert y1.data_ptr() == r.out.data_ptr() and y1.shape == (2, H)   # borrowed rows (moe_coop512.py:248)
     bad = to_dev(np.array([[0, 1], [2, 99]], np.int64), dev)   # 99 is outside the 12-entry table
     with pytest.raises(RuntimeError, match="outside"):
         r.run(x, bad, w, de.table, 3, 1.0)

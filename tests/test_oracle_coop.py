@@ -186,6 +186,11 @@ def test_activation_clamp_semantics():
     assert np.allclose(shared, [silu(10) * 10, silu(-30) * 3, silu(10) * -10, silu(0.5) * 0.25], rtol=1e-6)
     assert routed[0] != shared[0]
     assert np.array_equal(coop.act_gate(g, u, 0.0), (coop.silu_f32(g) * u).astype(np.float32))
+    # NaN: the routed kernel's fminf/fmaxf return the limit, torch.clamp keeps the NaN
+    nan = np.float32("nan")
+    assert coop.act_gate(np.array([nan], np.float32), np.array([nan], np.float32), 10.0)[0] == -100.0
+    assert np.isnan(coop.swiglu(np.array([nan], np.float32), np.array([1.0], np.float32), 10.0)[0])
+    assert np.isnan(coop.swiglu(np.array([1.0], np.float32), np.array([nan], np.float32), 10.0)[0])
 
 
 def test_moe_routed_linear_in_weights_and_sum_order():
@@ -224,3 +229,24 @@ def test_rel_err_rows_definition():
     ref = np.array([[1.0, -4.0, 0.0], [0.0, 0.0, 2.0]])
     y = ref + np.array([[0.04, 0.0, 0.0], [0.0, 0.01, 0.0]])
     assert math.isclose(coop.rel_err_rows(y, ref), 0.01)
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_clamp_orders_separate_at_the_test_limit(rows):
+    """At the GPU tests' clipping limit (0.75, unit-variance G and U) the reference layer, the
+    layer with the routed clamp moved before SiLU, the one with the shared clamp moved after
+    SiLU, and the unclamped one are all more than 5x the 1e-2 tolerance apart, so the GPU tests
+    that use this limit tell the clamp orders apart."""
+    from tests.gpu_helpers import clamp_variants
+    H, I, E, topk = 512, 256, 12, 4
+    rng = np.random.default_rng(20 + rows)
+    experts = [synth.expert(rng, H, I, 4, 1 / np.sqrt(H)) for _ in range(E)]
+    shared = synth.expert(rng, H, I, 4, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, rows, H)
+    logits = synth.logits_plain(rng, rows, E)
+    v = clamp_variants(lambda: coop.moe_layer(x, logits, experts, shared, topk, 0.75)[0])
+    for name in ("routed_swapped", "shared_swapped", "unclamped"):
+        assert coop.rel_err_rows(v[name], v["ref"]) > 5e-2, name
+    # and the limit of 10 used elsewhere never engages at these scales
+    v10 = clamp_variants(lambda: coop.moe_layer(x, logits, experts, shared, topk, 10.0)[0])
+    assert np.array_equal(v10["unclamped"], v10["ref"])
