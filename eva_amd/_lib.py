@@ -65,6 +65,7 @@ _SIGNATURES = {
     "evamx_moe_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(MoeShape)]),
     "evamx_moe_workspace_init": (ctypes.c_int, [ctypes.POINTER(MoeShape), _vp, _vp]),
     "evamx_moe_forward": (ctypes.c_int, [ctypes.POINTER(MoeArgs), _vp]),
+    "evamx_moe_forward_static": (ctypes.c_int, [ctypes.POINTER(MoeArgs), _vp]),
     "evamx_moe_runs_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_moe_flags_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_moe_logits_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),

@@ -101,7 +101,7 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.cap_rows_gu = L.ks_gu ? L.ks_gu * L.nslot_max : auto_rows;
     L.cap_rows_d = L.ks_d ? L.ks_d * L.nslot_max : auto_rows;
     size_t o = 0;
-    L.flags = o;   o = al256(o + 64 * 4);
+    L.flags = o;   o = al256(o + 64 * 4);     // first: evamx_moe_forward_static zeroes offset 0 of its scratch
     L.meta = o;    o = al256(o + 64 * 4);
     L.local = o;   o = al256(o + (size_t)L.slots_max * 4);
     L.order = o;   o = al256(o + (size_t)L.nslot_max * 4);

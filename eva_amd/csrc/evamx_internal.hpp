@@ -10,7 +10,8 @@ namespace evamx {
 void set_error(const char* fmt, ...);
 
 // The MoE forward of evamx_moe_forward on a given workspace (validation included); `who` names
-// the entry point in error messages.
+// the entry point in error messages. Used by the entry points with a caller's workspace and with
+// the library's fixed device scratch.
 int moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream,
                    const char* who);
 size_t moe_workspace_bytes_of(const evamx_moe_shape* shape);

@@ -332,6 +332,28 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     return out
 
 
+def moe_forward_static(shape: MoeShape, x: torch.Tensor, tables: torch.Tensor, out: torch.Tensor | None, *,
+                       limit: float, bits: float | None = None, k2_per_expert: torch.Tensor | None = None,
+                       logits: torch.Tensor | None = None, sel: torch.Tensor | None = None,
+                       weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
+                       score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
+                       shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1,
+                       max_expert: int = 0, events=None, residual: torch.Tensor | None = None,
+                       gate_w: torch.Tensor | None = None):
+    """``moe_forward`` without a workspace: evamx_moe_forward_static runs the layer on the
+    library's fixed device scratch (64 MiB per GPU) and allocates nothing, for callers that
+    cannot allocate (e.g. under graph capture). ``shape`` is the MoeShape a workspace would have
+    been built for. Calls that overlap on one GPU share the scratch and race."""
+    if not isinstance(x, torch.Tensor) or not x.is_cuda:
+        raise ValueError("x must be a device tensor")
+    a, keep = _moe_args(shape, x.device, x, tables, out, limit, bits, k2_per_expert, logits, sel, weights, rw,
+                        score_fn, sel_bias, route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events,
+                        residual, gate_w)
+    check(lib().evamx_moe_forward_static(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward_static")
+    del keep
+    return out
+
+
 def read_floor(ncg: int, rows: int, waves: int, device=None, reps: int = 50) -> float:
     """Bytes per second of the read-only benchmark (evamx_bench_read): ``waves`` waves stream
     ``rows`` 1 KiB chunks each in a decode GEMV launch's shape (wave w reads column group w % ncg

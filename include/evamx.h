@@ -162,6 +162,15 @@ typedef struct evamx_moe_args {
 } evamx_moe_args;
 
 size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape);
+/* No counterpart in the reference (its runners own their scratch tensors). For callers that
+ * cannot allocate device memory (code under hipGraph capture, serving loops that forbid
+ * hipMalloc): evamx_moe_forward with args->workspace == NULL and workspace_bytes == 0, run on
+ * the library's fixed device scratch of 64 MiB per GPU (held until the process ends). Shapes
+ * whose evamx_moe_workspace_bytes exceeds 64 MiB are rejected with EVAMX_ENOSPACE (DSv3 decode
+ * needs 44-53 MiB for 1-32 rows). Calls no allocator. All calls on one GPU share its scratch:
+ * calls that overlap on one GPU race. Device-side error flags are not reported by this entry
+ * point (flagged slots are skipped, as in evamx_moe_forward). */
+int evamx_moe_forward_static(const evamx_moe_args* args, evamx_stream_t stream);
 /* Zero the workspace's sticky flag word (a kernel, not a memset: capture-safe). Call once
  * after allocating the workspace. */
 int evamx_moe_workspace_init(const evamx_moe_shape* shape, void* workspace, evamx_stream_t stream);

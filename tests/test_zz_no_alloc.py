@@ -1,0 +1,76 @@
+"""evamx_moe_forward_static (the entry point that allocates nothing: the forward on the
+library's fixed device scratch) against evamx_moe_forward with a caller's workspace, through
+the C ABI: two calls in a row on the same GPU, the second with fewer rows, each bit-identical to
+the workspace path on the same inputs (same shape, so the same layout and work split), and the
+first also against the oracle. Plus the refusals: a shape too large for the scratch, and a
+workspace argument."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import coop, synth
+from tests.gpu_helpers import DeviceExperts, rel_err_rows, to_dev
+
+pytestmark = pytest.mark.gpu
+H, I, E, TOPK, ROWS_MAX = 512, 256, 24, 4, 16
+
+
+@pytest.fixture(scope="module")
+def case(dev):
+    rng = np.random.default_rng(808)
+    experts = [synth.expert(rng, H, I, 4, 1 / np.sqrt(H)) for _ in range(E)]
+    shared = synth.expert(rng, H, I, 4, 1 / np.sqrt(H))
+    return experts, shared, DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+
+
+def _run(ops, dev, case, x, logits, static):
+    experts, shared, de, ds = case
+    rows = x.shape[0]
+    sel = torch.full((rows, TOPK), -1, dtype=torch.int64, device=dev)
+    w = torch.full((rows, TOPK), -1.0, dtype=torch.float32, device=dev)
+    out = torch.full((rows, H), float("nan"), dtype=torch.float32, device=dev)
+    kw = dict(limit=0.75, bits=4, logits=to_dev(logits, dev), sel=sel, weights=w, shared_ptrs=ds.ptrs(0),
+              shared_bits=4)
+    xt = to_dev(x, dev).to(torch.bfloat16)
+    if static:
+        ops.moe_forward_static(ops.MoeShape(ROWS_MAX, H, I, TOPK, E, 1, 0, 0), xt, de.table, out, **kw)
+    else:
+        ws = ops.MoeWorkspace(dev, rows_max=ROWS_MAX, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True)
+        ws.buffer.fill_(0x7f)
+        ws.clear_flags()
+        ops.moe_forward(ws, xt, de.table, out, **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
+
+
+def test_static_scratch_matches_workspace_twice(dev, case):
+    from eva_amd import ops
+    experts, shared, _, _ = case
+    rng = np.random.default_rng(809)
+    for n, rows in enumerate((ROWS_MAX, 3)):                 # the second call is smaller
+        x = synth.activations_bf16(rng, rows, H)
+        logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
+        got = _run(ops, dev, case, x, logits, static=True)
+        want = _run(ops, dev, case, x, logits, static=False)
+        for g, w in zip(got, want):
+            assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
+                                  w.view(np.uint32) if w.dtype == np.float32 else w), (n, rows)
+        ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, TOPK, 0.75)
+        assert np.array_equal(got[1], ridx)
+        assert rel_err_rows(got[0], ref) < 1e-2
+
+
+def test_static_refusals(dev, case):
+    from eva_amd import _lib, ops
+    L = _lib.lib()
+    a = _lib.MoeArgs()
+    a.shape = _lib.MoeShape(4096, 7168, 2048, 8, 256, 1, 0, 0)     # a prefill-size workspace: too big
+    a.rows = 1
+    assert L.evamx_moe_forward_static(ctypes.byref(a), None) == _lib.EVAMX_ENOSPACE
+    assert b"fixed scratch" in L.evamx_last_error()
+    a.shape = _lib.MoeShape(1, H, I, TOPK, E, 0, 0, 0)
+    a.workspace = 1 << 20
+    a.workspace_bytes = 1 << 20
+    assert L.evamx_moe_forward_static(ctypes.byref(a), None) == _lib.EVAMX_EINVAL
