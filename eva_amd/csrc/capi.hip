@@ -40,8 +40,8 @@ static bool gemv_rate(int k2) { return gemv_k2_supported(k2); }   // 1.5 .. 4, 5
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t flags, meta, local, order, runs, chunks, unit_chunk, tiles, slot_mult, rw16, logits, xr, xsum, act, actsum, part_gu,
-        part_d, total;
+    size_t flags, meta, local, order, runs, chunks, unit_chunk, tiles, slot_mult, rw16, urec, srec, logits, xr, xsum, act,
+        actsum, part_gu, part_d, total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
 };
 
@@ -111,6 +111,12 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.tiles = o;   o = al256(o + (size_t)L.max_chunks * 4);
     L.slot_mult = o; o = al256(o + (size_t)L.nslot_max * 4);
     L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
+    {
+        // decode-path records: calls of at most EVAMX_GEMV_MAX_ROWS rows
+        const int dr = s->rows_max < EVAMX_GEMV_MAX_ROWS ? s->rows_max : EVAMX_GEMV_MAX_ROWS;
+        L.urec = o; o = al256(o + (size_t)(dr * s->topk + 1) * sizeof(UnitRec));
+        L.srec = o; o = al256(o + (size_t)dr * (s->topk + 1) * sizeof(SlotRec));
+    }
     L.logits = o;  o = al256(o + (size_t)s->rows_max * EVAMX_MAX_EXPERTS * 4);
     L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
     L.xsum = o;    o = al256(o + (size_t)2 * L.nslot_max * (s->hidden / 128) * 4);
@@ -413,6 +419,8 @@ int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t works
     p.unit_chunk = (int*)(ws + L.unit_chunk);
     p.tiles = (int*)(ws + L.tiles);
     p.slot_mult = (int*)(ws + L.slot_mult);
+    p.urec = (UnitRec*)(ws + L.urec);
+    p.srec = (SlotRec*)(ws + L.srec);
     p.max_chunks = L.max_chunks;
     p.xr = (half_t*)(ws + L.xr);
     p.xsum = (float*)(ws + L.xsum);

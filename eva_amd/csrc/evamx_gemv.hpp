@@ -211,9 +211,62 @@ struct GlobalRows {
     int sums_stride;        // chunks per row
 };
 
+// Activation source of gemv_wave: the 8 fp16 pairs (x[16kt + 2i], x[16kt + 2i + 1]) of row m
+// at k-slice kt. XScalar reads rows of global memory through wave-uniform addresses (scalar
+// loads into SGPRs); XLds reads rows the wave staged in LDS itself (one uniform-address
+// ds_read_b128 pair, a broadcast).
+template <int TM>
+struct XScalar {
+    const half2_t* A;
+    uint32_t aoff[TM];      // row m starts at A + 4 * aoff[m] (aoff in 16-byte units)
+    __device__ __forceinline__ void load(int m, int kt, half2_t (&d)[8]) const
+    {
+        const half2_t* xp = A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = xp[i];
+    }
+};
+
+// The rows are written and read as uint32_t words (one type, so that no alias rule separates
+// the wave's stores from its loads); rows and slices are 32-byte aligned, so the eight words of
+// a slice merge into wide LDS reads.
+struct XLds {
+    const uint32_t* base;   // LDS: row m at base + m * row_words, k-slice kt at word 8 * (kt - kt0)
+    int row_words;
+    int kt0;
+    __device__ __forceinline__ void load(int m, int kt, half2_t (&d)[8]) const
+    {
+        const uint32_t* xp = (const uint32_t*)__builtin_assume_aligned(base + m * row_words + 8 * (kt - kt0), 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = __builtin_bit_cast(half2_t, xp[i]);
+    }
+};
+
+// Orders a wave's LDS writes before its later LDS reads of other lanes' data (and its reads
+// before later overwrites): LDS instructions of one wave execute in order, the fence keeps the
+// compiler from moving them across.
+__device__ __forceinline__ void wave_lds_fence()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Work gemv_wave does around issuing its weight prefetch: issue() runs before the first weight
+// loads (loads issued there return first: vector memory loads return in order), finish() once
+// they are in flight.
+struct NoPrologue {
+    static constexpr bool kWork = false;
+    __device__ __forceinline__ void issue() {}
+    __device__ __forceinline__ void finish() {}
+};
+
 // ---------------------------------------------------------------------------------------------
-// Decode GEMV over one wave's k-range [16*kt0, 16*kt1): acc[m][h] = sum_k X[m][k] * h_k,
-// h_k = 1024 + bytesum of the weight at (k, col(lane, h)) (see mul1_hpair).
+// Decode GEMV over one wave's k-range [kt0, kt1): acc[m][h] += sum_k X[m][k] * h_k,
+// h_k = 1024 + bytesum of the weight at (k, col(lane, h)) (see mul1_hpair). The caller zeroes
+// acc. `prologue.issue()` runs just before the weight prefetch ring is issued and
+// `prologue.finish()` once it is in flight (the rotated-input path loads its activation words
+// first and stages its rows in LDS behind the latency of the first weight loads).
 
 // Weight prefetch depth (k-slices in flight per wave). Four slices (4 KiB per wave at 4 bpw)
 // measured best for every chunk width once the waves of a SIMD progress together (depths 4..10
@@ -221,9 +274,9 @@ struct GlobalRows {
 template <int TM>
 constexpr int prefetch_depth() { return 4; }
 
-template <int K2, int TM>
+template <int K2, int TM, typename XS, typename Pro>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
-                                          const GlobalRows& src, const uint32_t (&aoff)[TM], int tm, float (&acc)[TM][2])
+                                          const XS& xs, int tm, float (&acc)[TM][2], Pro& prologue)
 {
     using R = Rate<K2>;
     constexpr int K = R::K;
@@ -241,29 +294,25 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
     uint32_t lane_off, prev_off, sh;
     lane_offsets<K2>(lane, lane_off, prev_off, sh);
 
-#pragma unroll
-    for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = 0.0f;
-
     // Prefetch ring: the row PF slices ahead, clamped to the wave's last row so that the steady
     // state needs no branch and never reads outside the matrix (the clamped reloads hit cache).
+    prologue.issue();
     LaneWords<K> ring[PF];
     const int last = kt1 - 1;
 #pragma unroll
     for (int d = 0; d < PF; ++d) load_slice<K>(ring[d], rsrc, cbase + (uint32_t)min(kt0 + d, last) * slice, lane_off, prev_off);
+    // keep the prologue's work (and its waits for its own loads) after the ring is issued
+    if constexpr (Pro::kWork) __builtin_amdgcn_sched_barrier(0);
+    prologue.finish();
 
-    // Narrow chunks load the next slice's activations (wave-uniform, scalar loads) one step
-    // ahead, so their latency hides behind a decode instead of stalling every step.
+    // Narrow chunks load the next slice's activations one step ahead, so their latency hides
+    // behind a decode instead of stalling every step.
     constexpr bool XPF = TM <= 2;
     half2_t xa[TM][8];
     auto load_x = [&](half2_t (&dst)[TM][8], int kt) {
 #pragma unroll
-        for (int m = 0; m < TM; ++m) {
-            if (m < tm) {
-                const half2_t* xp = (const half2_t*)src.A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) dst[m][i] = xp[i];
-            }
-        }
+        for (int m = 0; m < TM; ++m)
+            if (m < tm) xs.load(m, kt, dst[m]);
     };
     if constexpr (XPF) load_x(xa, kt0);
 
@@ -279,11 +328,7 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
 #pragma unroll
         for (int m = 0; m < TM; ++m) {
             if (m < tm) {
-                if constexpr (!XPF) {
-                    const half2_t* xp = (const half2_t*)src.A + ((size_t)aoff[m] * 4 + (size_t)kt * 8);
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) xa[m][i] = xp[i];
-                }
+                if constexpr (!XPF) xs.load(m, kt, xa[m]);
                 float a0 = acc[m][0], a1 = acc[m][1];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -305,7 +350,7 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
 #pragma unroll
                 for (int i = 0; i < 8; ++i) xa[m][i] = xn[m][i];
         }
-        // keep the next step's scalar activation loads out of this one (register pressure)
+        // keep the next step's activation loads out of this one (register pressure)
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -337,12 +382,15 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
     const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
 #define EVAMX_RUN(TMV)                                                                          \
     {                                                                                           \
-        uint32_t aoff[TMV];                                                                     \
+        XScalar<TMV> xsrc;                                                                      \
+        xsrc.A = (const half2_t*)src.A;                                                         \
         _Pragma("unroll") for (int m = 0; m < TMV; ++m)                                         \
-            aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tr ? so[m] : so[0]) *        \
-                                                               (int)(src.stride / 8));          \
+            xsrc.aoff[m] = (uint32_t)__builtin_amdgcn_readfirstlane((m < tr ? so[m] : so[0]) *   \
+                                                                    (int)(src.stride / 8));     \
         float acc[TMV][2];                                                                      \
-        gemv_wave<K2, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, src, aoff, tr, acc);               \
+        _Pragma("unroll") for (int m = 0; m < TMV; ++m) acc[m][0] = acc[m][1] = 0.0f;           \
+        NoPrologue none;                                                                        \
+        gemv_wave<K2, TMV>(trellis, nt_n, cg, 8 * c0, 8 * c1, xsrc, tr, acc, none);              \
         _Pragma("unroll") for (int m = 0; m < TMV; ++m) {                                       \
             if (m < tr) {                                                                       \
                 const int row = so[m];                                                          \

@@ -25,6 +25,36 @@ enum {
 
 enum { PREP_GROUP = 1, PREP_MOE = 2 };
 
+// Calls of at most this many rows take the decode path (decode GEMVs, work resolved from records).
+constexpr int EVAMX_GEMV_MAX_ROWS = EVAMX_MFMA_MIN_ROWS - 1;
+
+// Records of the decode path, written by its prepare so that every later kernel resolves its
+// work with one load instead of a chain of dependent ones (unit -> chunk -> pointer table ->
+// weights). A GEMV wave reads its work unit's record; the activation and combine waves read
+// their slot's.
+constexpr int EVAMX_NO_UNIT = -2;
+struct alignas(128) UnitRec {
+    int e;                      // local expert, -1 the shared expert, EVAMX_NO_UNIT past the call's units
+    int rows;                   // rows (slots) of the unit's chunk, at most EVAMX_CHUNK
+    int k2;                     // 2 x bits
+    int ubase;                  // first unit of the chunk (a chunk of weight m owns m units)
+    int s_gu, s_d;              // k-splits of the chunk's gate/up and down GEMVs
+    int pad0[2];
+    int slot[EVAMX_CHUNK];      // the chunk's slots (entries past rows repeat slot[0])
+    uint64_t tr[3];             // gate, up, down trellis
+    uint64_t suh[2];            // gate, up input scales
+    uint64_t pad1[3];
+};
+struct alignas(64) SlotRec {
+    int active;                 // 0: an inactive slot (zero weight or outside the expert range)
+    int shared;                 // 1: a row of the shared expert
+    int s_gu, s_d;              // k-splits of the slot's chunk
+    float w;                    // routing weight as its fp16 value (1 for the shared expert)
+    int pad[3];
+    uint64_t g_svh, u_svh, d_suh, d_svh;
+};
+static_assert(sizeof(UnitRec) == 128 && sizeof(SlotRec) == 64, "record sizes");
+
 struct MoeParams {
     int mode;
     int mfma;                  // 1: expert GEMMs on the MFMA path (chunks of chunk_rows as tiles, each
@@ -79,6 +109,9 @@ struct MoeParams {
     int ks_gu_max, ks_d_max;   // bounds of the automatic choice
     int cap_rows_gu, cap_rows_d;   // partial-buffer capacity in rows (ks * nslot <= cap)
     int gemv_waves;            // grid of the GEMV kernels (waves resident on the device at once)
+    UnitRec* urec;             // decode path: [units_max] work-unit records
+    SlotRec* srec;             // decode path: [T * topk + T] slot records (routed slots, shared rows)
+    int units_max;             // decode path: work units the launch grids cover (T * topk + has_shared)
     // output
     float* out;                // or null
     int out_stride;
@@ -87,13 +120,13 @@ struct MoeParams {
 };
 
 // Rows of the GEMV partial buffers in this call: the routed slots, then the shared expert's rows.
-__device__ __forceinline__ int moe_nslot(const MoeParams& p) { return p.T * p.topk + (p.has_shared ? p.T : 0); }
+__host__ __device__ __forceinline__ int moe_nslot(const MoeParams& p) { return p.T * p.topk + (p.has_shared ? p.T : 0); }
 
 // Cost weight of a chunk of `rows` rows: its decode is shared by the rows, each row adds its dot
 // products, so a chunk of 8 rows costs about three chunks of one. Work is handed out in units
 // of weight 1; a chunk of weight m gets m times the k-splits of a one-row chunk.
 constexpr int EVAMX_MAX_MULT = 3;
-__device__ __forceinline__ int chunk_mult(int rows) { return rows <= 3 ? 1 : rows <= 6 ? 2 : 3; }
+__host__ __device__ __forceinline__ int chunk_mult(int rows) { return rows <= 3 ? 1 : rows <= 6 ? 2 : 3; }
 
 // K-split choice of a GEMV: `base` splits per work unit, as many as fill the resident grid once
 // (or the requested count), a chunk of weight m gets min(base * m, cap) splits (base when the
@@ -103,7 +136,7 @@ struct KSplit {
     int base, cap;
 };
 
-__device__ __forceinline__ KSplit moe_ksplit(int req, int items_per_split, int waves, int kmax, int cap_rows, int nslot)
+__host__ __device__ __forceinline__ KSplit moe_ksplit(int req, int items_per_split, int waves, int kmax, int cap_rows, int nslot)
 {
     KSplit k;
     k.cap = cap_rows / nslot < kmax ? cap_rows / nslot : kmax;
@@ -119,7 +152,7 @@ __device__ __forceinline__ KSplit moe_ksplit(int req, int items_per_split, int w
     return k;
 }
 
-__device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
+__host__ __device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
 {
     const int v = k.base * mult;
     return v < k.cap ? v : k.cap;
@@ -130,7 +163,7 @@ __device__ __forceinline__ int ks_of_chunk(const KSplit& k, int mult)
 // VALU as busy as four, and half the waves halve the prologues and the partials the next stage
 // sums (T=1 82.4 -> 79.6 us); with more rows per chunk two waves per SIMD lose (T=2 116 -> 122,
 // T=4 174 -> 255 us).
-__device__ __forceinline__ int split_waves(const MoeParams& p)
+__host__ __device__ __forceinline__ int split_waves(const MoeParams& p)
 {
     return (!p.mfma && p.T == 1) ? p.gemv_waves / 2 : p.gemv_waves;
 }
@@ -138,7 +171,7 @@ __device__ __forceinline__ int split_waves(const MoeParams& p)
 // MFMA gate/up tiles that leave part of one resident round empty unsplit take two splits: with
 // items < waves per split, SIMDs hold 3 or 4 equal items, and the ones with 4 set the launch's
 // time; two splits even that out (16 tokens at DSv3: gate/up 228-230 -> 224-225 us).
-__device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
+__host__ __device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
 {
     const int items = units * 2 * (p.I / 128);
     KSplit k = moe_ksplit(p.ks_gu, items, split_waves(p), p.ks_gu_max, p.cap_rows_gu, moe_nslot(p));
@@ -146,7 +179,7 @@ __device__ __forceinline__ KSplit ks_gate_up(const MoeParams& p, int units)
     return k;
 }
 
-__device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
+__host__ __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units)
 {
     return moe_ksplit(p.ks_d, units * (p.H / 128), split_waves(p), p.ks_d_max, p.cap_rows_d, moe_nslot(p));
 }

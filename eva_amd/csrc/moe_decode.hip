@@ -737,6 +737,215 @@ __global__ __launch_bounds__(64 * EVAMX_SMALL_ROWS) void moe_prepare_small_kerne
 }
 
 // ---------------------------------------------------------------------------------------------
+// Prepare of the decode path (calls of at most EVAMX_GEMV_MAX_ROWS rows): one workgroup routes,
+// groups, publishes the run table and writes the unit and slot records; the input rotations
+// happen inside the gate/up GEMV waves, each for its own k-range.
+
+// Bitonic sort of one 32-bit key per lane across the wave, ascending in lane order: stages on
+// lane bits (size 2..64, stride size/2..1), each a compare-exchange with lane ^ stride.
+template <int SIZE, int STRIDE>
+__device__ __forceinline__ uint32_t bitonic_stage(uint32_t k, int lane)
+{
+    const uint32_t o = xor_lane<STRIDE>(k, lane);
+    const bool up = (lane & SIZE) == 0;                 // ascending block (SIZE 64: all lanes)
+    const bool lower = (lane & STRIDE) == 0;
+    return (lower == up) ? (k < o ? k : o) : (k > o ? k : o);
+}
+
+template <int SIZE, int STRIDE>
+__device__ __forceinline__ uint32_t bitonic_merge(uint32_t k, int lane)
+{
+    k = bitonic_stage<SIZE, STRIDE>(k, lane);
+    if constexpr (STRIDE > 1) k = bitonic_merge<SIZE, STRIDE / 2>(k, lane);
+    return k;
+}
+
+__device__ __forceinline__ uint32_t wave_sort_asc(uint32_t k, int lane)
+{
+    k = bitonic_merge<2, 1>(k, lane);
+    k = bitonic_merge<4, 2>(k, lane);
+    k = bitonic_merge<8, 4>(k, lane);
+    k = bitonic_merge<16, 8>(k, lane);
+    k = bitonic_merge<32, 16>(k, lane);
+    k = bitonic_merge<64, 32>(k, lane);
+    return k;
+}
+
+// Prepare of the decode path (calls of at most EVAMX_GEMV_MAX_ROWS rows, so at most 64 slots):
+// waves [0, T) route one token each while the other waves copy the [9][n_local] pointer table
+// (and the per-expert rates) into LDS; then wave 0 alone groups the slots with one key per lane
+// sorted across the wave (key (local expert, slot): the stable order by expert), cuts runs of at
+// most EVAMX_CHUNK slots at expert changes (the reference run table's runs, which are also the
+// GEMV chunks), and writes the run table and the unit and slot records from registers and LDS.
+constexpr int GEMV_PREP_WAVES = 4;
+
+struct GemvPrepLds {
+    uint64_t tbl[9][EVAMX_MAX_EXPERTS];
+    uint8_t k2[EVAMX_MAX_EXPERTS];
+    int sel[64];
+    half_t rw[64];
+};
+
+__global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(MoeParams p)
+{
+    __shared__ GemvPrepLds sh;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int slots = p.T * p.topk;               // at most 2 * EVAMX_MAX_TOPK = 64
+    const int E = p.n_local;
+    if (p.runs) {
+        const int table_len = 2 + 2 * p.slots_max + 1;
+        for (int i = t; i < table_len; i += blockDim.x) p.runs[i] = 0;
+    }
+    if (wave < p.T) {
+        if (p.logits) route_token(p, wave, lane, sh.sel, sh.rw, true);      // writes slots wave * topk + j
+    } else {
+        const int nt = (GEMV_PREP_WAVES - p.T) * 64, i0 = t - p.T * 64;
+        for (int i = i0; i < 9 * E; i += nt) sh.tbl[i / E][i % E] = (uint64_t)p.tables[(size_t)(i / E) * p.tbl_stride + i % E];
+        if (p.k2_per_expert)
+            for (int i = i0; i < E; i += nt) sh.k2[i] = p.k2_per_expert[i];
+    }
+    if (!p.logits && t < slots) {
+        const int64_t e = p.sel[t];
+        sh.sel[t] = (e >= 0 && e < 0x7fffffff) ? (int)e : -1;
+        sh.rw[t] = p.weights ? f2h(p.weights[t]) : p.rw16[t];
+        if (p.weights) p.rw16[t] = sh.rw[t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    // slot activity (lane = slot), the published local expert, inactive slot records
+    int e = -1;
+    if (lane < slots) {
+        e = slot_local(p, sh.sel[lane], sh.rw[lane], true);
+        p.local[lane] = e;
+        if (e < 0) {
+            SlotRec q = {};
+            p.srec[lane] = q;
+        }
+    }
+    // stable grouping: sort keys (expert, slot); inactive slots sort last
+    const uint32_t key = wave_sort_asc(e >= 0 ? ((uint32_t)e << 6) | (uint32_t)lane : 0xffffffffu, lane);
+    const bool act = key != 0xffffffffu;
+    const int ge = (int)(key >> 6), gs = (int)(key & 63);
+    const uint64_t amask = __ballot(act);
+    const int n_active = __popcll(amask);
+    const int prev_e = __shfl_up(ge, 1, WAVE);
+    const uint64_t heads = __ballot(act && (lane == 0 || prev_e != ge));
+    const uint64_t le_mask = lane == 63 ? ~0ull : ((2ull << lane) - 1);     // lanes 0..lane
+    const int first = 63 - __clzll(heads & le_mask);                        // the expert's first position
+    const bool rs = act && ((lane - first) % EVAMX_CHUNK) == 0;             // run (chunk) start
+    const uint64_t rmask = __ballot(rs);
+    const int n_runs = __popcll(rmask);
+    const uint64_t above = rmask & ~le_mask;
+    const int next = above ? __ffsll((long long)above) - 1 : n_active;
+    const int rows = rs ? next - lane : 0;
+    const int m = rs ? chunk_mult(rows) : 0;
+    const int m_incl = wave_incl_scan(m);
+    const int ubase = m_incl - m;
+    const int routed_units = __builtin_amdgcn_readlane(m_incl, 63);
+    const KSplit kgu = ks_gate_up(p, p.units_max), kd = ks_down(p, p.units_max);
+    // the chunk of each position: its run start's lane
+    const int rlane = act ? 63 - __clzll(rmask & le_mask) : 0;
+    const int my_m = __shfl(m, rlane, WAVE);
+    int slot_run[EVAMX_CHUNK];
+#pragma unroll
+    for (int j = 0; j < EVAMX_CHUNK; ++j) slot_run[j] = __shfl(gs, lane + j < 64 ? lane + j : 63, WAVE);
+
+    if (act) {
+        // run table (moe_coop3072.py:86-106): order, run starts
+        if (p.runs) {
+            p.runs[2 + p.slots_max + 1 + lane] = gs;
+            if (rs) p.runs[2 + __popcll(rmask & (le_mask >> 1)) ] = lane;
+        }
+        p.order[lane] = gs;
+        const int k2 = p.k2_per_expert ? (int)sh.k2[ge] : p.k2_uniform;
+        SlotRec q;
+        q.active = 1;
+        q.shared = 0;
+        q.s_gu = ks_of_chunk(kgu, my_m);
+        q.s_d = ks_of_chunk(kd, my_m);
+        q.w = h2f(sh.rw[gs]);
+        q.pad[0] = q.pad[1] = q.pad[2] = 0;
+        q.g_svh = sh.tbl[EVAMX_TBL_G_SVH][ge];
+        q.u_svh = sh.tbl[EVAMX_TBL_U_SVH][ge];
+        q.d_suh = sh.tbl[EVAMX_TBL_D_SUH][ge];
+        q.d_svh = sh.tbl[EVAMX_TBL_D_SVH][ge];
+        p.srec[gs] = q;
+        if (rs) {
+            if (!gemv_k2_supported(k2)) atomicOr(p.err, EVAMX_ERR_RATE);
+            UnitRec r;
+            r.e = ge;
+            r.rows = rows;
+            r.k2 = k2;
+            r.ubase = ubase;
+            r.s_gu = ks_of_chunk(kgu, m);
+            r.s_d = ks_of_chunk(kd, m);
+            r.pad0[0] = r.pad0[1] = 0;
+#pragma unroll
+            for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = j < rows ? slot_run[j] : slot_run[0];
+            r.tr[0] = sh.tbl[EVAMX_TBL_G_TRELLIS][ge];
+            r.tr[1] = sh.tbl[EVAMX_TBL_U_TRELLIS][ge];
+            r.tr[2] = sh.tbl[EVAMX_TBL_D_TRELLIS][ge];
+            r.suh[0] = sh.tbl[EVAMX_TBL_G_SUH][ge];
+            r.suh[1] = sh.tbl[EVAMX_TBL_U_SUH][ge];
+            r.pad1[0] = r.pad1[1] = r.pad1[2] = 0;
+            for (int i = 0; i < m; ++i) p.urec[ubase + i] = r;
+        }
+    }
+    // the shared expert: one chunk of the T rows after the routed ones
+    int n_units = routed_units;
+    if (p.has_shared) {
+        if (lane < p.T) {
+            p.order[n_active + lane] = slots + lane;
+            SlotRec q;
+            q.active = 1;
+            q.shared = 1;
+            q.s_gu = ks_of_chunk(kgu, 1);
+            q.s_d = ks_of_chunk(kd, 1);
+            q.w = 1.0f;
+            q.pad[0] = q.pad[1] = q.pad[2] = 0;
+            q.g_svh = (uint64_t)p.sh_ptr[EVAMX_TBL_G_SVH];
+            q.u_svh = (uint64_t)p.sh_ptr[EVAMX_TBL_U_SVH];
+            q.d_suh = (uint64_t)p.sh_ptr[EVAMX_TBL_D_SUH];
+            q.d_svh = (uint64_t)p.sh_ptr[EVAMX_TBL_D_SVH];
+            p.srec[slots + lane] = q;
+        }
+        if (lane == 0) {
+            UnitRec r;
+            r.e = -1;
+            r.rows = p.T;
+            r.k2 = p.k2_shared;
+            r.ubase = routed_units;
+            r.s_gu = ks_of_chunk(kgu, 1);
+            r.s_d = ks_of_chunk(kd, 1);
+            r.pad0[0] = r.pad0[1] = 0;
+#pragma unroll
+            for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = slots + (j < p.T ? j : 0);
+            r.tr[0] = (uint64_t)p.sh_ptr[EVAMX_TBL_G_TRELLIS];
+            r.tr[1] = (uint64_t)p.sh_ptr[EVAMX_TBL_U_TRELLIS];
+            r.tr[2] = (uint64_t)p.sh_ptr[EVAMX_TBL_D_TRELLIS];
+            r.suh[0] = (uint64_t)p.sh_ptr[EVAMX_TBL_G_SUH];
+            r.suh[1] = (uint64_t)p.sh_ptr[EVAMX_TBL_U_SUH];
+            r.pad1[0] = r.pad1[1] = r.pad1[2] = 0;
+            p.urec[routed_units] = r;
+        }
+        n_units += 1;      // T <= 2 rows: one chunk of weight 1
+    }
+    for (int u = n_units + lane; u < p.units_max; u += 64) p.urec[u].e = EVAMX_NO_UNIT;
+    if (lane == 0) {
+        if (p.runs) {
+            p.runs[0] = n_runs;
+            p.runs[1] = 0;
+            p.runs[2 + n_runs] = n_active;
+        }
+        p.meta[0] = n_runs + (p.has_shared ? 1 : 0);
+        p.meta[1] = n_active;
+        p.meta[2] = n_units;
+        p.meta[3] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Prepare for any batch, in three launches: routing (one wave per token), grouping (one
 // workgroup of 1024 threads, per-slot arrays in global memory), rotations (a full grid).
 
@@ -796,43 +1005,322 @@ __device__ __forceinline__ const void* expert_ptr(const MoeParams& p, int e, int
     return (const void*)p.tables[(size_t)row * p.tbl_stride + e];
 }
 
-// Gate/up GEMV: one wave per work item (chunk, 128 columns, gate|up, k-split) ->
-// part_gu[ks][proj][slot][I].
-template <int TMAX>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_kernel(MoeParams p, const half_t* __restrict__ xr)
+// ---------------------------------------------------------------------------------------------
+// Decode path (calls of at most EVAMX_GEMV_MAX_ROWS rows): gate/up waves rotate their own
+// inputs. A wave (unit, gate|up, 128 columns, k-split) reads its unit's record, issues its
+// weight prefetch, and while the first weight loads are in flight computes fp16(H128(x * suh))
+// of its rows over its k-chunks into LDS (with each row's chunk sums, added in chunk order),
+// then streams the weights against those LDS rows. The k-range is taken in windows of at most
+// ROT_CW chunks (one window at the DSv3 shape).
+
+constexpr int ROT_CW = 16;            // 128-chunks of rotated input per LDS window and row
+
+// Rotations of the tm rows so[0..tm) over the 128-chunks [w0, w1) into LDS (row m at dst + m *
+// row_words, chunk w0 + j at word 64 j), adding each chunk's sum to xs[m]: the operations of
+// rotate_chunks, so rows and sums are bit-identical to the rotation kernels' output. issue()
+// loads the x and suh words of the first ROT_BATCH chunks, finish() rotates and stores them
+// (and any further chunks of the window, loading them then).
+template <int TM>
+struct RotStage {
+    static constexpr bool kWork = true;
+    const MoeParams& p;
+    const int (&so)[TM];
+    int tm, w0, w1, row_words, lane;
+    __amdgpu_buffer_rsrc_t suh_rsrc, x_rsrc[TM];   // wave-uniform bases: loads take scalar offsets
+    uint32_t* dst;
+    float (&xs)[TM];
+    uint32_t xv[TM][ROT_BATCH], sv[ROT_BATCH];
+
+    __device__ __forceinline__ void load(int b)
+    {
+        // chunk c of a row is 256 bytes at byte 256 c, lane l's pair at byte 4 l; chunks past the
+        // window reload its last one (in bounds, unused), so the loads need no branches
+#pragma unroll
+        for (int j = 0; j < ROT_BATCH; ++j)
+            sv[j] = __builtin_amdgcn_raw_buffer_load_b32(suh_rsrc, 4 * lane, 256 * min(b + j, w1 - 1), 0);
+#pragma unroll
+        for (int m = 0; m < TM; ++m)
+#pragma unroll
+            for (int j = 0; j < ROT_BATCH; ++j)
+                xv[m][j] = __builtin_amdgcn_raw_buffer_load_b32(x_rsrc[m], 4 * lane, 256 * min(b + j, w1 - 1), 0);
+    }
+    __device__ __forceinline__ void rotate(int b)
+    {
+        const int slots = p.T * p.topk;
+#pragma unroll
+        for (int m = 0; m < TM; ++m) {
+            if (m >= tm) continue;
+            const bool shared = so[m] >= slots;
+            uint32_t* d = dst + m * row_words + lane;
+#pragma unroll
+            for (int j = 0; j < ROT_BATCH; ++j) {
+                if (b + j < w1) {
+                    const half2_t su = __builtin_bit_cast(half2_t, sv[j]);
+                    float v0 = x_elem(xv[m][j], 0, p.x_dtype) * h2f(su.x);
+                    float v1 = x_elem(xv[m][j], 1, p.x_dtype) * h2f(su.y);
+                    if (shared) {
+                        // shared EXL3 linear: fp16 product (hadamard_inner.cuh:109-115)
+                        v0 = h2f(f2h(v0));
+                        v1 = h2f(f2h(v1));
+                    }
+                    had128_pair(v0, v1, lane);
+                    const half2_t r = {f2h(v0), f2h(v1)};
+                    d[(b + j - w0) * 64] = __builtin_bit_cast(uint32_t, r);
+                    xs[m] += wave_sum(h2f(r.x) + h2f(r.y));
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void issue() { load(w0); }
+    __device__ __forceinline__ void finish()
+    {
+        rotate(w0);
+        for (int b = w0 + ROT_BATCH; b < w1; b += ROT_BATCH) {
+            load(b);
+            rotate(b);
+        }
+        wave_lds_fence();
+    }
+};
+
+// The same rotations shared by the four waves of a workgroup, which then stream four column
+// groups of the same (unit, projection, k-split): wave w rotates chunks w, w + 4, ... of the
+// window into the workgroup's LDS rows and stores each chunk's sum; after a barrier every wave
+// adds the sums in chunk order (the order of the per-wave stage, so the results are the same).
+constexpr int ROT_WAVES = 4;
+
+template <int TM>
+struct RotStageGroup {
+    static constexpr bool kWork = true;
+    static constexpr int NJ = ROT_CW / ROT_WAVES;     // chunks per wave and window
+    const MoeParams& p;
+    const int (&so)[TM];
+    int tm, w0, w1, row_words, lane, wave;
+    __amdgpu_buffer_rsrc_t suh_rsrc, x_rsrc[TM];
+    uint32_t* dst;                                      // LDS rows
+    float* sums;                                        // LDS [TM][ROT_CW] chunk sums
+    float (&xs)[TM];
+    uint32_t xv[TM][NJ], sv[NJ];
+
+    __device__ __forceinline__ int chunk(int i) const { return min(w0 + wave + ROT_WAVES * i, w1 - 1); }
+    __device__ __forceinline__ void issue()
+    {
+#pragma unroll
+        for (int i = 0; i < NJ; ++i) sv[i] = __builtin_amdgcn_raw_buffer_load_b32(suh_rsrc, 4 * lane, 256 * chunk(i), 0);
+#pragma unroll
+        for (int m = 0; m < TM; ++m)
+#pragma unroll
+            for (int i = 0; i < NJ; ++i) xv[m][i] = __builtin_amdgcn_raw_buffer_load_b32(x_rsrc[m], 4 * lane, 256 * chunk(i), 0);
+    }
+    __device__ __forceinline__ void finish()
+    {
+        const int slots = p.T * p.topk;
+#pragma unroll
+        for (int m = 0; m < TM; ++m) {
+            if (m >= tm) continue;
+            const bool shared = so[m] >= slots;
+#pragma unroll
+            for (int i = 0; i < NJ; ++i) {
+                const int c = w0 + wave + ROT_WAVES * i;
+                if (c < w1) {
+                    const half2_t su = __builtin_bit_cast(half2_t, sv[i]);
+                    float v0 = x_elem(xv[m][i], 0, p.x_dtype) * h2f(su.x);
+                    float v1 = x_elem(xv[m][i], 1, p.x_dtype) * h2f(su.y);
+                    if (shared) {
+                        v0 = h2f(f2h(v0));
+                        v1 = h2f(f2h(v1));
+                    }
+                    had128_pair(v0, v1, lane);
+                    const half2_t r = {f2h(v0), f2h(v1)};
+                    dst[m * row_words + (c - w0) * 64 + lane] = __builtin_bit_cast(uint32_t, r);
+                    const float sm = wave_sum(h2f(r.x) + h2f(r.y));
+                    if (lane == 0) sums[m * ROT_CW + (c - w0)] = sm;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < TM; ++m)
+            if (m < tm)
+                for (int c = 0; c < w1 - w0; ++c) xs[m] += sums[m * ROT_CW + c];
+    }
+};
+
+// Gate/up GEMV of tm rows (slots slot[0..tm)) over the 128-chunks [c0, c1): each window of at
+// most ROT_CW chunks is rotated into LDS (GROUP: by the workgroup's four waves together), then
+// streamed; writes the fp32 partials of the rows.
+template <int K2, int TM, bool GROUP>
+__device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
+                                                 const int* slot, int tm, int cg, int c0, int c1, float* part,
+                                                 uint32_t* lds, float* lsums)
 {
+    const int lane = threadIdx.x & 63;
+    // the record is not written during this kernel: scalar loads of its slots
+    const __attribute__((address_space(4))) int* sl = (const __attribute__((address_space(4))) int*)slot;
+    int so[TM];
+#pragma unroll
+    for (int m = 0; m < TM; ++m) so[m] = __builtin_amdgcn_readfirstlane(sl[m < tm ? m : 0]);
+    float acc[TM][2], xs[TM];
+#pragma unroll
+    for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = xs[m] = 0.0f;
+    constexpr int RW = ROT_CW * 64;
+    const int slots = p.T * p.topk;
+    __amdgpu_buffer_rsrc_t xrs[TM];
+#pragma unroll
+    for (int m = 0; m < TM; ++m) {
+        const int row = so[m] >= slots ? so[m] - slots : so[m] / p.topk;
+        xrs[m] = weight_rsrc((const uint32_t*)((const uint16_t*)p.x + (size_t)row * p.x_stride));
+    }
+    const __amdgpu_buffer_rsrc_t srs = weight_rsrc((const uint32_t*)suh);
+    auto window = [&](int w0, int w1) {
+        const XLds src{lds, RW, 8 * w0};
+        if constexpr (GROUP) {
+            RotStageGroup<TM> stage{p, so, tm, w0, w1, RW, lane, (int)(threadIdx.x >> 6), srs, {}, lds, lsums, xs};
+#pragma unroll
+            for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
+            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+        } else {
+            RotStage<TM> stage{p, so, tm, w0, w1, RW, lane, srs, {}, lds, xs};
+#pragma unroll
+            for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
+            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+        }
+    };
+    if (c1 - c0 <= ROT_CW) {
+        window(c0, c1);                 // the common case, straight-line
+    } else {
+        for (int w0 = c0; w0 < c1; w0 += ROT_CW) {
+            window(w0, min(c1, w0 + ROT_CW));
+            // this window's reads before the next window's writes
+            if constexpr (GROUP) __syncthreads();
+            else wave_lds_fence();
+        }
+    }
+    const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
+#pragma unroll
+    for (int m = 0; m < TM; ++m) {
+        if (m < tm) {
+            float* dst = part + (size_t)so[m] * p.I;
+            dst[col0] = MUL1_K_INV * acc[m][0] + MUL1_K_BIAS * xs[m];
+            dst[col1] = MUL1_K_INV * acc[m][1] + MUL1_K_BIAS * xs[m];
+        }
+    }
+}
+
+template <int K2, int TMAX, bool GROUP>
+__device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
+                                                 const int* slot, int rows, int cg, int c0, int c1, float* part,
+                                                 uint32_t* lds, float* lsums)
+{
+    if (rows <= TMAX) {                 // the common case, straight-line
+        if constexpr (TMAX == 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
+        else if (rows <= 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
+        else gate_up_rot_rows<K2, 2, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
+        return;
+    }
+    // a chunk of more than TMAX rows (given routes that repeat an expert) runs TMAX rows at a time
+    for (int r0 = 0; r0 < rows; r0 += TMAX) {
+        const int tr = rows - r0 < TMAX ? rows - r0 : TMAX;
+        if constexpr (TMAX == 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+        else {
+            static_assert(TMAX == 2, "decode path rows: 1 or 2");
+            if (tr <= 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+            else gate_up_rot_rows<K2, 2, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+        }
+        if constexpr (GROUP) __syncthreads();      // this pass's LDS reads before the next pass's writes
+        else wave_lds_fence();
+    }
+}
+
+// One wave per (unit, gate|up, k-split, 128 columns). GROUP (the column-group count a multiple
+// of 4): the items run column group fastest, so the four waves of a workgroup share unit,
+// projection and k-split (and exit together) and rotate their inputs together; otherwise every
+// wave rotates its own.
+template <int TMAX, bool GROUP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_rot_kernel(MoeParams p)
+{
+    __shared__ uint32_t xl[GROUP ? 1 : 4][TMAX * ROT_CW * 64];
+    __shared__ float xsums[TMAX * ROT_CW];
+    const int wave = threadIdx.x >> 6;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
     const int ncg = p.I / 128;
-    const KSplit k = ks_gate_up(p, units);
+    const KSplit k = ks_gate_up(p, p.units_max);
     const int per_unit = 2 * ncg * k.base;
-    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * 2 * ncg * ks)
     const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
-    if (u >= units) return;
-    const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
-    const int* ch = p.chunks + 8 * ci;
-    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-    const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
-    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
-    const int ubase = __builtin_amdgcn_readfirstlane(ch[4]);
-    const int S = ks_of_chunk(k, __builtin_amdgcn_readfirstlane(ch[5]));
+    if (u >= p.units_max) return;
+    const UnitRec* rp = p.urec + u;
+    const int e = __builtin_amdgcn_readfirstlane(rp->e);
+    if (e == EVAMX_NO_UNIT) return;
+    const int ubase = __builtin_amdgcn_readfirstlane(rp->ubase);
+    const int S = __builtin_amdgcn_readfirstlane(rp->s_gu);
     const int r = wid - ubase * per_unit;
     if (r >= 2 * ncg * S) return;
-    // integer division runs on the vector ALU: pin the (uniform) results to scalar registers
-    const int cg = __builtin_amdgcn_readfirstlane(r / (2 * S));
-    const int rem = r % (2 * S);
-    const int proj = __builtin_amdgcn_readfirstlane(rem / S), ks = __builtin_amdgcn_readfirstlane(rem % S);
-    const int* slot_of = p.order + begin;
-
+    int cg, proj, ks;
+    if constexpr (GROUP) {
+        cg = __builtin_amdgcn_readfirstlane(r % ncg);
+        const int pk = r / ncg;
+        proj = __builtin_amdgcn_readfirstlane(pk / S);
+        ks = __builtin_amdgcn_readfirstlane(pk % S);
+    } else {
+        cg = __builtin_amdgcn_readfirstlane(r / (2 * S));
+        const int rem = r % (2 * S);
+        proj = __builtin_amdgcn_readfirstlane(rem / S);
+        ks = __builtin_amdgcn_readfirstlane(rem % S);
+    }
+    const int rows = __builtin_amdgcn_readfirstlane(rp->rows);
+    const int k2 = __builtin_amdgcn_readfirstlane(rp->k2);
     const int nch = p.H / 128;
-    const int nslot = moe_nslot(p);
     const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
-    const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, proj == 0 ? EVAMX_TBL_G_TRELLIS : EVAMX_TBL_U_TRELLIS);
-    const GlobalRows src{xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch,
-                         nch};
-    float* part = p.part_gu + ((size_t)ks * 2 + proj) * nslot * p.I;
-    gemv_dispatch_k<TMAX>(k2, trellis, p.I / 16, cg, c0, c1, src, slot_of, tm, part, (size_t)p.I);
+    const uint32_t* trellis = (const uint32_t*)rp->tr[proj];
+    const half_t* suh = (const half_t*)rp->suh[proj];
+    float* part = p.part_gu + ((size_t)ks * 2 + proj) * moe_nslot(p) * p.I;
+    uint32_t* lds = xl[GROUP ? 0 : wave];
+    switch (k2) {
+        case 3: gate_up_rot_item<3, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        case 4: gate_up_rot_item<4, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        case 5: gate_up_rot_item<5, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        case 6: gate_up_rot_item<6, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        case 7: gate_up_rot_item<7, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        case 8: gate_up_rot_item<8, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        case 10: gate_up_rot_item<10, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+        default: {
+            // unsupported rate (flagged by the prepare): zero partials, so no output reads stale data
+            const int lane = threadIdx.x & 63;
+            for (int m = 0; m < rows; ++m) {
+                float* dst = part + (size_t)rp->slot[m] * p.I + cg * 128;
+                dst[lane_col(lane, 0)] = 0.0f;
+                dst[lane_col(lane, 1)] = 0.0f;
+            }
+        }
+    }
+}
+
+// Down GEMV of the decode path: one wave per (unit, 128 columns, k-split), from the unit's record.
+template <int TMAX>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_down_rec_kernel(MoeParams p)
+{
+    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int ncg = p.H / 128;
+    const KSplit k = ks_down(p, p.units_max);
+    const int per_unit = ncg * k.base;
+    const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
+    if (u >= p.units_max) return;
+    const UnitRec* rp = p.urec + u;
+    const int e = __builtin_amdgcn_readfirstlane(rp->e);
+    if (e == EVAMX_NO_UNIT) return;
+    const int ubase = __builtin_amdgcn_readfirstlane(rp->ubase);
+    const int S = __builtin_amdgcn_readfirstlane(rp->s_d);
+    const int r = wid - ubase * per_unit;
+    if (r >= ncg * S) return;
+    const int cg = __builtin_amdgcn_readfirstlane(r / S), ks = __builtin_amdgcn_readfirstlane(r % S);
+    const int rows = __builtin_amdgcn_readfirstlane(rp->rows);
+    const int k2 = __builtin_amdgcn_readfirstlane(rp->k2);
+    const int na = p.I / 128;
+    const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
+    const uint32_t* trellis = (const uint32_t*)rp->tr[2];
+    float* part = p.part_d + (size_t)ks * moe_nslot(p) * p.H;
+    gemv_dispatch_k<TMAX>(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{p.act, (size_t)p.I, p.actsum, na}, rp->slot,
+                          rows, part, (size_t)p.H);
 }
 
 // Fixed-order sums over the k-splits q = 0..S-1 of N values per lane, value n at
@@ -865,26 +1353,42 @@ __device__ __forceinline__ void sum_splits(const float* const (&base)[N], size_t
 // 784-805 for routed slots (act_gate with the clamp after SiLU) or the shared expert's EXL3
 // linear outputs + swiglu (model.py:450-452, kernels.py:213-217), and the down projection's
 // input rotation; writes act (fp16) and the chunk's sum.
-template <int CPW>
+// REC (decode path): waves are (slot, chunk group), every slot's work resolved from its record
+// (inactive slots exit); otherwise (grouped row, chunk group) over the call's active rows.
+template <int CPW, bool REC>
 __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
 {
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int na = p.I / 128;
     const int ng = na / CPW;                 // chunk groups per row (CPW divides na)
-    const int n_rows = p.meta[1] + (p.has_shared ? p.T : 0);
+    const int n_rows = REC ? moe_nslot(p) : p.meta[1] + (p.has_shared ? p.T : 0);
     if (wid >= n_rows * ng) return;
     const int o = wid / ng, a0 = (wid % ng) * CPW;
-    const int slots = p.T * p.topk;
-    const int s = __builtin_amdgcn_readfirstlane(p.order[o]);
-    const int e = s < slots ? __builtin_amdgcn_readfirstlane(p.local[s]) : -1;
-    const bool shared = e < 0;
-    const half_t* g_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_G_SVH);
-    const half_t* u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
-    const half_t* d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
+    int s, Sg;
+    bool shared;
+    const half_t *g_svh, *u_svh, *d_suh;
+    if constexpr (REC) {
+        s = o;
+        const SlotRec* rp = p.srec + s;
+        if (!__builtin_amdgcn_readfirstlane(rp->active)) return;
+        shared = __builtin_amdgcn_readfirstlane(rp->shared) != 0;
+        Sg = __builtin_amdgcn_readfirstlane(rp->s_gu);
+        g_svh = (const half_t*)rp->g_svh;
+        u_svh = (const half_t*)rp->u_svh;
+        d_suh = (const half_t*)rp->d_suh;
+    } else {
+        const int slots = p.T * p.topk;
+        s = __builtin_amdgcn_readfirstlane(p.order[o]);
+        const int e = s < slots ? __builtin_amdgcn_readfirstlane(p.local[s]) : -1;
+        shared = e < 0;
+        g_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_G_SVH);
+        u_svh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_U_SVH);
+        d_suh = (const half_t*)expert_ptr(p, e, EVAMX_TBL_D_SUH);
+        Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
+                         __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
+    }
     const float L = p.limit;
-    const int Sg = ks_of_chunk(ks_gate_up(p, __builtin_amdgcn_readfirstlane(p.meta[2])),
-                               __builtin_amdgcn_readfirstlane(p.slot_mult[s]));
     const int nslot = moe_nslot(p);
     // all chunks' scales and partial sums first, so their loads are in flight together
     float g[CPW][2], u[CPW][2], gs[CPW][2], us[CPW][2], ds[CPW][2];
@@ -962,47 +1466,16 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
 static void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
 {
     const int na = p.I / 128;
-    if (p.T > EVAMX_SMALL_ROWS && na % 4 == 0) {
+    if (p.T <= EVAMX_GEMV_MAX_ROWS) {
+        const int waves = nslot * na;
+        launch_timed(moe_act_kernel<1, true>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
+    } else if (p.T > EVAMX_SMALL_ROWS && na % 4 == 0) {
         const int waves = nslot * (na / 4);
-        launch_timed(moe_act_kernel<4>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
+        launch_timed(moe_act_kernel<4, false>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
     } else {
         const int waves = nslot * na;
-        launch_timed(moe_act_kernel<1>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
+        launch_timed(moe_act_kernel<1, false>, dim3((waves + 3) / 4), dim3(256), stream, start, stop, p);
     }
-}
-
-// Down GEMV: one wave per work item (chunk, 128 columns, k-split) -> part_d[ks][slot][H].
-template <int TMAX>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_down_kernel(MoeParams p, const half_t* __restrict__ act)
-{
-    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
-    const int ncg = p.H / 128;
-    const KSplit k = ks_down(p, units);
-    const int per_unit = ncg * k.base;
-    // one item per wave: the launch covers max(gemv_waves, EVAMX_MAX_MULT * max_chunks * ncg * ks)
-    const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
-    if (u >= units) return;
-    const int ci = __builtin_amdgcn_readfirstlane(p.unit_chunk[u]);
-    const int* ch = p.chunks + 8 * ci;
-    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-    const int tm = __builtin_amdgcn_readfirstlane(ch[2]);
-    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
-    const int ubase = __builtin_amdgcn_readfirstlane(ch[4]);
-    const int S = ks_of_chunk(k, __builtin_amdgcn_readfirstlane(ch[5]));
-    const int r = wid - ubase * per_unit;
-    if (r >= ncg * S) return;
-    const int cg = __builtin_amdgcn_readfirstlane(r / S), ks = __builtin_amdgcn_readfirstlane(r % S);
-    const int* slot_of = p.order + begin;
-
-    const int na = p.I / 128;
-    const int nslot = moe_nslot(p);
-    const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
-    const uint32_t* trellis = (const uint32_t*)expert_ptr(p, e, EVAMX_TBL_D_TRELLIS);
-    float* part = p.part_d + (size_t)ks * nslot * p.H;
-    gemv_dispatch_k<TMAX>(k2, trellis, p.H / 16, cg, c0, c1, GlobalRows{act, (size_t)p.I, p.actsum, na}, slot_of, tm,
-                          part, (size_t)p.H);
 }
 
 // Sum of the down k-split partials of slot s on this lane's two columns, fixed order; loads of
@@ -1069,6 +1542,8 @@ __device__ __forceinline__ void combine_store(const MoeParams& p, int row, int c
 // together, then the svh pointer and the partials, so an item costs two memory round trips.
 constexpr int EVAMX_COMBINE_WAVES = 16;
 
+// REC (decode path): an item's activity, weight, split count and svh come from its slot record.
+template <bool REC>
 __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(MoeParams p)
 {
     __shared__ float part[EVAMX_MAX_TOPK + 1][128];
@@ -1083,18 +1558,33 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
     for (int k = wave; k < nitems; k += nw) {
         const bool shared = k == p.topk;
         const int sk = shared ? slots + row : row * p.topk + k;
-        const int le = shared ? -1 : __builtin_amdgcn_readfirstlane(p.local[sk]);
-        const int mult = __builtin_amdgcn_readfirstlane(p.slot_mult[sk]);
-        const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
-        const float w = shared ? 1.0f : h2f(p.rw16[sk]);
-        if (!shared && le < 0) {
-            if (lane == 0) active[k] = 0;
-            continue;
+        float w;
+        int S;
+        const half_t* svh;
+        if constexpr (REC) {
+            const SlotRec* rp = p.srec + sk;
+            if (!__builtin_amdgcn_readfirstlane(rp->active)) {
+                if (lane == 0) active[k] = 0;
+                continue;
+            }
+            w = rp->w;
+            S = __builtin_amdgcn_readfirstlane(rp->s_d);
+            svh = (const half_t*)rp->d_svh;
+        } else {
+            const int le = shared ? -1 : __builtin_amdgcn_readfirstlane(p.local[sk]);
+            const int mult = __builtin_amdgcn_readfirstlane(p.slot_mult[sk]);
+            const int units = __builtin_amdgcn_readfirstlane(p.meta[2]);
+            w = shared ? 1.0f : h2f(p.rw16[sk]);
+            if (!shared && le < 0) {
+                if (lane == 0) active[k] = 0;
+                continue;
+            }
+            svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
+                         : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
+            S = ks_of_chunk(ks_down(p, units), mult);
         }
-        const half_t* svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
-                                   : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
         float v[2];
-        sum_partials(p, sk, cg, lane, ks_of_chunk(ks_down(p, units), mult), v);
+        sum_partials(p, sk, cg, lane, S, v);
         combine_item(shared, w, h2f(svh[col0]), h2f(svh[col1]), v, lane);
         part[k][c0] = v[0];
         part[k][c1] = v[1];
@@ -1203,6 +1693,9 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     // up to 16 tokens only the 16-row MFMA kernel runs, so the tiles are cut at 16 rows (more
     // than 16 slots of one expert occur only when given routes repeat an expert within a token)
     p.chunk_rows = !p.mfma ? EVAMX_CHUNK : p.T <= EVAMX_SMALL_TILE_ROWS ? EVAMX_SMALL_TILE_ROWS : EVAMX_TILE_ROWS;
+    // decode path: chunks of at most 8 rows weigh at most their row count, so the call has at
+    // most one unit per slot plus the shared expert's one (its rows fit one chunk)
+    p.units_max = p.T * p.topk + (p.has_shared ? 1 : 0);
     hipEvent_t first = ev(0);
     if (p.gate_w) {
         const int waves = p.n_logits * ((p.T + GATE_ROWS - 1) / GATE_ROWS);
@@ -1210,7 +1703,11 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
                      const_cast<float*>(p.logits));
         first = nullptr;
     }
-    if (small) {
+    if (!p.mfma) {
+        // decode path: one workgroup routes, groups and writes the records; the gate/up waves
+        // rotate their own inputs
+        launch_timed(moe_prepare_gemv_kernel, dim3(1), dim3(256), stream, first, ev(1), p);
+    } else if (small) {
         // workgroup 0 groups, the others rotate; a wave per token routes in every workgroup
         // at most one workgroup per CU (gemv_waves = 16 per CU), so that none waits for a slot
         const int nwv = p.T > 4 ? p.T : 4;
@@ -1237,25 +1734,32 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         // (a chunk with more rows, from routes that repeat an expert, runs two rows at a time)
         const int tmax = p.T <= 1 ? 1 : 2;
         {
-            // one wave per item: a requested split gives every chunk exactly ks_gu splits, an
-            // automatic one fits the resident grid (moe_ksplit)
-            const long units = (long)EVAMX_MAX_MULT * p.max_chunks * 2 * (p.I / 128) * (p.ks_gu > 0 ? p.ks_gu : 1);
-            const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
-            const half_t* xr = p.xr;
-            if (tmax == 1) launch_timed(moe_gate_up_kernel<1>, grid, dim3(256), stream, ev(2), ev(3), p, xr);
-            else launch_timed(moe_gate_up_kernel<2>, grid, dim3(256), stream, ev(2), ev(3), p, xr);
+            // one wave per item (unit, gate|up, 128 columns, k-split) over the launch's fixed
+            // unit count; waves of units past the call's exit at once
+            const long waves = (long)p.units_max * 2 * (p.I / 128) * ks_gate_up(p, p.units_max).base;
+            const dim3 grid((unsigned)((waves + 3) / 4));
+            const bool group = (p.I / 128) % ROT_WAVES == 0;
+            if (tmax == 1) {
+                if (group) launch_timed(moe_gate_up_rot_kernel<1, true>, grid, dim3(256), stream, ev(2), ev(3), p);
+                else launch_timed(moe_gate_up_rot_kernel<1, false>, grid, dim3(256), stream, ev(2), ev(3), p);
+            } else {
+                if (group) launch_timed(moe_gate_up_rot_kernel<2, true>, grid, dim3(256), stream, ev(2), ev(3), p);
+                else launch_timed(moe_gate_up_rot_kernel<2, false>, grid, dim3(256), stream, ev(2), ev(3), p);
+            }
         }
         launch_act(p, nslot, stream, ev(4), ev(5));
-        const long units = (long)EVAMX_MAX_MULT * p.max_chunks * (p.H / 128) * (p.ks_d > 0 ? p.ks_d : 1);
-        const dim3 grid((unsigned)(((units > p.gemv_waves ? units : p.gemv_waves) + 3) / 4));
-        const half_t* act = p.act;
-        if (tmax == 1) launch_timed(moe_down_kernel<1>, grid, dim3(256), stream, ev(6), ev(7), p, act);
-        else launch_timed(moe_down_kernel<2>, grid, dim3(256), stream, ev(6), ev(7), p, act);
+        const long waves = (long)p.units_max * (p.H / 128) * ks_down(p, p.units_max).base;
+        const dim3 grid((unsigned)((waves + 3) / 4));
+        if (tmax == 1) launch_timed(moe_down_rec_kernel<1>, grid, dim3(256), stream, ev(6), ev(7), p);
+        else launch_timed(moe_down_rec_kernel<2>, grid, dim3(256), stream, ev(6), ev(7), p);
     }
     if (p.T <= EVAMX_SMALL_ROWS) {
         int nw = p.topk + (p.has_shared ? 1 : 0);
         if (nw > EVAMX_COMBINE_WAVES) nw = EVAMX_COMBINE_WAVES;
-        launch_timed(moe_combine_kernel, dim3(p.T * (p.H / 128)), dim3(64 * nw), stream, ev(8), ev(9), p);
+        if (!p.mfma)
+            launch_timed(moe_combine_kernel<true>, dim3(p.T * (p.H / 128)), dim3(64 * nw), stream, ev(8), ev(9), p);
+        else
+            launch_timed(moe_combine_kernel<false>, dim3(p.T * (p.H / 128)), dim3(64 * nw), stream, ev(8), ev(9), p);
     } else {
         launch_timed(moe_combine_rows_kernel, dim3((p.T * (p.H / 128) + 3) / 4), dim3(256), stream, ev(8), ev(9), p);
     }

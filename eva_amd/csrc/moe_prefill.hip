@@ -32,13 +32,6 @@ constexpr int MF_WAVES = 4;                     // waves per workgroup
 constexpr int MF_LDS_WORDS = 8 * 64 * 4;        // per wave: 8 B operands x 64 lanes x 16 bytes
 constexpr int MF_PF = 4;                        // k-slices of weight prefetch (two MFMA k-steps)
 
-__device__ __forceinline__ void wave_lds_fence()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // One work item: rows [0, rows) (slots slot_of[0..rows)) of activations src (fp16 [slot][K]
 // with 128-chunk sums) times the decoded weights of tiles 8*cg .. 8*cg+7 of a projection over
 // the k-slices [kt0, kt1) (whole 128-chunks); writes part[slot * part_stride + 128 * cg +
