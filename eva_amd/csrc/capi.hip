@@ -180,7 +180,7 @@ extern "C" int evamx_exl3_dequant(const void* trellis, int in_features, int out_
 
 extern "C" size_t evamx_exl3_linear_workspace_bytes(int rows, int in_features, int out_features)
 {
-    if (rows < 1 || in_features < 128 || out_features < 128) return 0;
+    if (rows < 1 || rows > 65536 || in_features < 128 || out_features < 128) return 0;
     return linear_workspace(rows, in_features, out_features, nullptr, nullptr);
 }
 
@@ -191,7 +191,7 @@ extern "C" int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, 
     g_err[0] = 0;
     const int k2 = rate_k2(bits);
     EVAMX_REQUIRE(x_fp16 && trellis && suh_fp16 && svh_fp16 && y_fp16 && workspace, "evamx_exl3_linear: null pointer");
-    EVAMX_REQUIRE(rows >= 1 && rows <= 16, "evamx_exl3_linear: rows %d outside 1..16", rows);
+    EVAMX_REQUIRE(rows >= 1 && rows <= 65536, "evamx_exl3_linear: rows %d outside 1..65536", rows);
     EVAMX_REQUIRE(in_features >= 128 && out_features >= 128 && in_features % 128 == 0 && out_features % 128 == 0,
                   "evamx_exl3_linear: in/out (%d, %d) must be positive multiples of 128", in_features, out_features);
     EVAMX_REQUIRE(gemv_rate(k2), "evamx_exl3_linear: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)bits);

@@ -274,14 +274,13 @@ struct NoPrologue {
 template <int TM>
 constexpr int prefetch_depth() { return 4; }
 
-template <int K2, int TM, typename XS, typename Pro>
+template <int K2, int TM, int PF = prefetch_depth<TM>(), typename XS, typename Pro>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
                                           const XS& xs, int tm, float (&acc)[TM][2], Pro& prologue)
 {
     using R = Rate<K2>;
     constexpr int K = R::K;
     constexpr int TW = R::TW;
-    constexpr int PF = prefetch_depth<TM>();
     const int lane = threadIdx.x & 63;
     // the k-range is wave-uniform: keep it (and all index math below) in scalar registers
     kt0 = __builtin_amdgcn_readfirstlane(kt0);

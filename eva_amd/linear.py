@@ -1,18 +1,17 @@
 """Drop-in EXL3 linear: ``ELinear`` / ``build_linear`` of runtime/ds41/exl3_linear.py:64-154,
 forwarding to evamx_exl3_linear (fp16 in, fp16 out, the reference's rounding points).
 
-Each row's result is independent of how many rows share the call (the k-split and the
-per-row accumulation order depend only on in/out), which is the batch-invariance the
-reference's strict small-row mode obtains by running rows one at a time
-(exl3_linear.py:106-127). Rows are processed 16 per launch.
+Calls of up to 16 rows take the decode GEMV; larger calls take the MFMA path (the reference
+likewise runs small batches row by row and hands larger ones to its GEMM, exl3_linear.py:106-128).
+Within each path a row's result is independent of how many rows share the call (the k-split and
+the per-row accumulation order depend only on in/out): the batch invariance the reference's
+strict small-row mode obtains by running rows one at a time.
 """
 from __future__ import annotations
 
 import torch
 
 from . import ops
-
-MAX_ROWS_PER_LAUNCH = 16
 
 
 class ELinear:
@@ -41,10 +40,7 @@ class ELinear:
         if flat.shape[-1] != self.in_features:
             raise ValueError("input width differs from the EXL3 metadata")
         y = torch.empty(flat.shape[0], self.out_features, dtype=torch.float16, device=flat.device)
-        for s in range(0, flat.shape[0], MAX_ROWS_PER_LAUNCH):
-            part = flat[s:s + MAX_ROWS_PER_LAUNCH]
-            ops.exl3_linear(part, self.trellis, self.suh, self.svh, self.k, out=y[s:s + part.shape[0]],
-                            workspace=self._workspace(part.shape[0]))
+        ops.exl3_linear(flat, self.trellis, self.suh, self.svh, self.k, out=y, workspace=self._workspace(flat.shape[0]))
         return y.reshape(*shape[:-1], self.out_features)
 
     __call__ = forward

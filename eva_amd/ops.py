@@ -50,7 +50,8 @@ def exl3_dequant(trellis: torch.Tensor, bits: float) -> torch.Tensor:
 
 def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bits: float,
                 out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """Single EXL3 linear, fp16 ``x [M, in]`` (M <= 16) -> fp16 ``[M, out]``."""
+    """Single EXL3 linear, fp16 ``x [M, in]`` -> fp16 ``[M, out]`` (decode GEMV up to 16 rows, MFMA
+    tiles beyond)."""
     _dev(x, "x", torch.float16, 2)
     _dev(trellis, "trellis", torch.int16, 3)
     _dev(suh, "suh", torch.float16, 1)

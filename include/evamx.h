@@ -61,7 +61,9 @@ int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, f
 size_t evamx_exl3_linear_workspace_bytes(int rows, int in_features, int out_features);
 
 /* y[rows][out] = svh * H(W^T H(x * suh)) with the reference's fp16 rounding points.
- * rows in 1..16; in/out multiples of 128; bits in {1.5,2,2.5,3,3.5,4,5}. All pointers device. */
+ * rows in 1..65536 (up to 16 rows a decode GEMV, beyond it MFMA tiles; within each a row's result
+ * does not depend on how many rows share the call); in/out multiples of 128; bits in
+ * {1.5,2,2.5,3,3.5,4,5}. All pointers device. */
 int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, int out_features,
                       const void* trellis, const void* suh_fp16, const void* svh_fp16, float bits,
                       void* y_fp16, void* workspace, size_t workspace_bytes, evamx_stream_t stream);

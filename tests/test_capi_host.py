@@ -121,7 +121,8 @@ def test_other_entry_points_reject_bad_arguments():
     L = _lib.lib()
     assert L.evamx_exl3_dequant(FAKE, 2048, 7168, 4.25, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_exl3_dequant(FAKE, 2040, 7168, 4.0, FAKE, None) == _lib.EVAMX_EINVAL
-    assert L.evamx_exl3_linear(FAKE, 17, 2048, 7168, FAKE, FAKE, FAKE, 4.0, FAKE, FAKE, 1 << 30, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_exl3_linear(FAKE, 65537, 2048, 7168, FAKE, FAKE, FAKE, 4.0, FAKE, FAKE, 1 << 40, None) == _lib.EVAMX_EINVAL
+    assert L.evamx_exl3_linear(FAKE, 0, 2048, 7168, FAKE, FAKE, FAKE, 4.0, FAKE, FAKE, 1 << 30, None) == _lib.EVAMX_EINVAL
     assert L.evamx_exl3_linear(FAKE, 1, 2048, 7168, FAKE, FAKE, FAKE, 4.0, FAKE, FAKE, 16, None) == _lib.EVAMX_ENOSPACE
     assert L.evamx_route_topk(FAKE, 0, 1, 256, 300, 0, 1.0, FAKE, FAKE, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_route_topk(FAKE, 0, 1, 600, 8, 0, 1.0, FAKE, FAKE, FAKE, None) == _lib.EVAMX_EINVAL

@@ -36,6 +36,17 @@ def test_config1_linear(dev):
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
 
 
+def test_config1_linear_128_rows(dev):
+    """configs[0]'s layer at 128 rows (the MFMA path of the linear) against the oracle."""
+    from eva_amd import ops
+    rng = np.random.default_rng(111)
+    tr, suh, svh = synth.projection(rng, 2048, 7168, 4)
+    x = synth.activations_bf16(rng, 128, 2048).astype(np.float16)
+    y = ops.exl3_linear(to_dev(x, dev), to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), 4).cpu().numpy()
+    ref = coop.exl3_linear(x, tr, suh, svh, 4)
+    assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
+
+
 def _moe(ops, dev, H, I, E, topk, rows, experts_dev, k2, x, logits, shared_dev=None, shared_bits=None, limit=10.0):
     ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E,
                           has_shared=shared_dev is not None)

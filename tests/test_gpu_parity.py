@@ -94,6 +94,20 @@ def test_exl3_linear(dev, K, rows):
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
 
 
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
+@pytest.mark.parametrize("rows", [17, 64, 100])
+def test_exl3_linear_mfma_path(dev, K, rows):
+    """More than 16 rows: input rotation, then MFMA tiles whose waves sum their k-ranges in LDS
+    and run the output epilogue (tiles of 17..64 rows and a ragged last tile)."""
+    ops = _ops()
+    rng = np.random.default_rng(200 + rows)
+    tr, suh, svh = synth.projection(rng, 1024, 384, K, svh_scale=1 / np.sqrt(1024))
+    x = rng.standard_normal((rows, 1024)).astype(np.float16)
+    y = ops.exl3_linear(to_dev(x, dev), to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), K).cpu().numpy()
+    ref = coop.exl3_linear(x, tr, suh, svh, K)
+    assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
+
+
 def _layer_case(rng, H, I, E, K, svh_scale, rates=None):
     experts = []
     for e in range(E):
