@@ -13,7 +13,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library resolves against)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libevamx.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EVAMX_OK, EVAMX_EINVAL, EVAMX_ELAUNCH, EVAMX_ENOSPACE = 0, -1, -2, -3
 DTYPE_F16, DTYPE_BF16 = 0, 1
@@ -37,7 +37,9 @@ class MoeArgs(ctypes.Structure):
                 ("min_expert", _i32), ("max_expert", _i32), ("tables", _vp), ("k2_per_expert", _vp),
                 ("bits", _f32), ("shared", _vp), ("shared_bits", _f32), ("limit", _f32),
                 ("out", _vp), ("out_stride", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
-                ("events", _vp), ("residual", _vp), ("residual_stride", _i32), ("gate_w", _vp)]
+                ("events", _vp), ("residual", _vp), ("residual_stride", _i32), ("gate_w", _vp),
+                ("bits_down", _f32), ("k2_down_per_expert", _vp), ("shared_bits_down", _f32),
+                ("shared_gate_w", _vp)]
 
 
 class EvamxError(RuntimeError):

@@ -42,6 +42,7 @@ class ResidentExperts:
         # [L, 9, N] pointer tables and [L, N] rates (2 x bits) of the resident layers, in layer order
         self.packed = torch.stack([self._layers[l].table for l in self.layer_ids])
         self.k2 = torch.stack([self._layers[l].k2 for l in self.layer_ids])
+        self.k2_down = torch.stack([self._layers[l].k2_down for l in self.layer_ids])
         self._pos = {l: i for i, l in enumerate(self.layer_ids)}
         self._rates = {l: set(self._layers[l].k2_host) for l in self.layer_ids}
         self._ws = {}
@@ -60,7 +61,7 @@ class ResidentExperts:
         if layer not in self._pos:
             raise KeyError(f"layer {layer} is not resident (loaded: {self.layer_ids})")
         i = self._pos[layer]
-        return self.packed[i], self.k2[i]
+        return self.packed[i], self.k2[i], self.k2_down[i]
 
     def _check(self, x, k, inter):
         if inter is not None and inter != self.inter:
@@ -80,7 +81,7 @@ class ResidentExperts:
         """Routed experts of ``layer`` for given routes: fp32 ``[rows, hidden]`` (cache.py:2276).
         ``indices`` int ``[..., topk]`` (local expert ids), ``weights`` float ``[..., topk]``."""
         self._check(x, k, inter)
-        table, k2 = self._layer(layer)
+        table, k2, k2d = self._layer(layer)
         self._check_rate(layer, k)
         x2 = x.reshape(-1, self.hidden)
         if x2.dtype not in (torch.float16, torch.bfloat16):
@@ -92,7 +93,8 @@ class ResidentExperts:
         ws = self._workspace(rows, topk, False)
         if out is None:
             out = torch.empty(rows, self.hidden, dtype=torch.float32, device=self.device)
-        ops.moe_forward(ws, x2.contiguous(), table, out, limit=float(limit), k2_per_expert=k2, sel=sel, weights=w)
+        ops.moe_forward(ws, x2.contiguous(), table, out, limit=float(limit), k2_per_expert=k2, k2_down_per_expert=k2d,
+                        sel=sel, weights=w)
         return out
 
     def moe_step(self, layer, x, logits=None, *, gate_w=None, limit=0.0, score_fn="sigmoid", sel_bias=None,
@@ -104,7 +106,7 @@ class ResidentExperts:
         may be ``x``) the output is added into it in place. Returns ``(out, sel, weights)``;
         capturable into a hipGraph (no host synchronisation)."""
         self._check(x, None, None)
-        table, k2 = self._layer(layer)
+        table, k2, k2d = self._layer(layer)
         rows = x.shape[0]
         ws = self._workspace(rows, self.topk, shared is not None)
         if sel is None:
@@ -115,7 +117,8 @@ class ResidentExperts:
             out = torch.empty(rows, self.hidden, dtype=torch.float32, device=self.device)
         if (logits is None) == (gate_w is None):
             raise ValueError("give logits or gate_w")
-        ops.moe_forward(ws, x, table, out, limit=float(limit), k2_per_expert=k2, logits=logits, gate_w=gate_w,
+        ops.moe_forward(ws, x, table, out, limit=float(limit), k2_per_expert=k2, k2_down_per_expert=k2d,
+                        logits=logits, gate_w=gate_w,
                         sel=sel, weights=weights, score_fn=score_fn, sel_bias=sel_bias, route_scale=route_scale,
                         shared_ptrs=shared, shared_bits=shared_bits, residual=residual)
         return out, sel, weights

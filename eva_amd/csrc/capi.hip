@@ -40,8 +40,8 @@ static bool gemv_rate(int k2) { return gemv_k2_supported(k2); }   // 1.5 .. 4, 5
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t flags, meta, local, order, runs, chunks, unit_chunk, tiles, slot_mult, rw16, urec, srec, logits, xr, xsum, act,
-        actsum, part_gu, part_d, total;
+    size_t flags, meta, local, order, runs, chunks, unit_chunk, tiles, slot_mult, rw16, urec, srec, gate_val, logits, xr,
+        xsum, act, actsum, part_gu, part_d, total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
 };
 
@@ -117,6 +117,7 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
         L.urec = o; o = al256(o + (size_t)(dr * s->topk + 1) * sizeof(UnitRec));
         L.srec = o; o = al256(o + (size_t)dr * (s->topk + 1) * sizeof(SlotRec));
     }
+    L.gate_val = o; o = al256(o + (size_t)s->rows_max * 4);
     L.logits = o;  o = al256(o + (size_t)s->rows_max * EVAMX_MAX_EXPERTS * 4);
     L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
     L.xsum = o;    o = al256(o + (size_t)2 * L.nslot_max * (s->hidden / 128) * 4);
@@ -163,7 +164,7 @@ using namespace evamx;
 
 extern "C" const char* evamx_last_error(void) { return g_err; }
 
-extern "C" int evamx_abi_version(void) { return 3; }
+extern "C" int evamx_abi_version(void) { return 4; }
 
 extern "C" int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, float bits, void* w_fp16,
                                   evamx_stream_t stream)
@@ -375,13 +376,26 @@ int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t works
         k2u = rate_k2(a->bits);
         EVAMX_REQUIRE(gemv_rate(k2u), "%s: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", who, (double)a->bits);
     }
-    int k2s = 0;
+    int k2du = 0;                  // 0: the down rate follows the gate/up rate
+    if (!a->k2_down_per_expert && a->bits_down != 0.0f) {
+        k2du = rate_k2(a->bits_down);
+        EVAMX_REQUIRE(gemv_rate(k2du), "%s: down bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", who, (double)a->bits_down);
+    }
+    int k2s = 0, k2sd = 0;
     if (s->has_shared) {
         EVAMX_REQUIRE(a->shared, "%s: shape has a shared expert but no pointers were given", who);
         for (int i = 0; i < 9; ++i) EVAMX_REQUIRE(a->shared[i] != 0, "%s: shared pointer %d is null", who, i);
         k2s = rate_k2(a->shared_bits);
         EVAMX_REQUIRE(gemv_rate(k2s), "%s: shared bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", who, (double)a->shared_bits);
+        k2sd = k2s;
+        if (a->shared_bits_down != 0.0f) {
+            k2sd = rate_k2(a->shared_bits_down);
+            EVAMX_REQUIRE(gemv_rate(k2sd), "%s: shared down bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", who,
+                          (double)a->shared_bits_down);
+        }
     }
+    EVAMX_REQUIRE(!a->shared_gate_w || s->has_shared, "%s: shared_gate_w without a shared expert", who);
+    EVAMX_REQUIRE(((uintptr_t)a->shared_gate_w & 3) == 0, "%s: shared_gate_w must be 4-byte aligned", who);
     if (workspace_bytes < L.total) {
         set_error("%s: workspace %zu bytes < %zu", who, workspace_bytes, L.total);
         return EVAMX_ENOSPACE;
@@ -405,6 +419,9 @@ int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t works
     p.max_expert = a->max_expert;
     p.tables = a->tables; p.tbl_stride = s->n_local;
     p.k2_per_expert = a->k2_per_expert; p.k2_uniform = k2u; p.k2_shared = k2s;
+    p.k2d_per_expert = a->k2_down_per_expert; p.k2d_uniform = k2du; p.k2_shared_d = k2sd;
+    p.sh_gate_w = (const half_t*)a->shared_gate_w;
+    p.gate_val = (float*)(ws + L.gate_val);
     p.has_shared = s->has_shared ? 1 : 0;
     if (s->has_shared)
         for (int i = 0; i < 9; ++i) p.sh_ptr[i] = a->shared[i];

@@ -36,10 +36,11 @@ constexpr int EVAMX_NO_UNIT = -2;
 struct alignas(128) UnitRec {
     int e;                      // local expert, -1 the shared expert, EVAMX_NO_UNIT past the call's units
     int rows;                   // rows (slots) of the unit's chunk, at most EVAMX_CHUNK
-    int k2;                     // 2 x bits
+    int k2;                     // 2 x bits of gate and up
     int ubase;                  // first unit of the chunk (a chunk of weight m owns m units)
     int s_gu, s_d;              // k-splits of the chunk's gate/up and down GEMVs
-    int pad0[2];
+    int k2_d;                   // 2 x bits of down
+    int pad0;
     int slot[EVAMX_CHUNK];      // the chunk's slots (entries past rows repeat slot[0])
     uint64_t tr[3];             // gate, up, down trellis
     uint64_t suh[2];            // gate, up input scales
@@ -79,6 +80,11 @@ struct MoeParams {
     int tbl_stride;
     const uint8_t* k2_per_expert;
     int k2_uniform, k2_shared;
+    const uint8_t* k2d_per_expert;   // down rates per expert, or null
+    int k2d_uniform;                 // uniform down rate when k2d_per_expert is null (0: the gate/up rate)
+    int k2_shared_d;                 // the shared expert's down rate
+    const half_t* sh_gate_w;         // gated shared expert: fp16 [H], or null
+    float* gate_val;                 // [rows]: sigmoid(x_row . sh_gate_w), written by the activation stage
     int has_shared;
     int64_t sh_ptr[9];
     float limit;
@@ -88,8 +94,8 @@ struct MoeParams {
     int* order;                // [slots + T]
     int* runs;                 // reference run table [2 + 2*slots_max + 1]
     int slots_max;
-    int* chunks;               // [max_chunks][8]: expert (-1 shared), begin, rows, k2, first unit,
-                               // units (cost weight of the chunk, chunk_mult), 0, 0
+    int* chunks;               // [max_chunks][8]: expert (-1 shared), begin, rows, gate/up k2, first
+                               // unit, units (cost weight of the chunk, chunk_mult), down k2, 0
     int max_chunks;
     int* unit_chunk;           // [EVAMX_MAX_MULT * max_chunks]: work unit -> chunk
     int* tiles;                // [max_chunks] MFMA tiles by size, each class in expert order: those
@@ -118,6 +124,19 @@ struct MoeParams {
     uint16_t* residual;        // bf16, updated in place, or null
     int residual_stride;
 };
+
+// Rates (2 x bits) of local expert e (-1: the shared expert): gate/up, and down (the down tables
+// or uniform rate when given, else the gate/up rate).
+__device__ __forceinline__ int k2_gu_of(const MoeParams& p, int e)
+{
+    return e < 0 ? p.k2_shared : p.k2_per_expert ? (int)p.k2_per_expert[e] : p.k2_uniform;
+}
+__device__ __forceinline__ int k2_d_of(const MoeParams& p, int e)
+{
+    if (e < 0) return p.k2_shared_d;
+    if (p.k2d_per_expert) return (int)p.k2d_per_expert[e];
+    return p.k2d_uniform ? p.k2d_uniform : k2_gu_of(p, e);
+}
 
 // Rows of the GEMV partial buffers in this call: the routed slots, then the shared expert's rows.
 __host__ __device__ __forceinline__ int moe_nslot(const MoeParams& p) { return p.T * p.topk + (p.has_shared ? p.T : 0); }

@@ -533,11 +533,11 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             c[0] = e;
             c[1] = ex.off[e] + j * CR;
             c[2] = rows;
-            c[3] = p.k2_per_expert ? (int)p.k2_per_expert[e] : p.k2_uniform;
-            if (!gemv_k2_supported(c[3]) && j == 0) atomicOr(p.err, EVAMX_ERR_RATE);
+            c[3] = k2_gu_of(p, e);
+            c[6] = k2_d_of(p, e);
+            if ((!gemv_k2_supported(c[3]) || !gemv_k2_supported(c[6])) && j == 0) atomicOr(p.err, EVAMX_ERR_RATE);
             c[4] = u;
             c[5] = m;
-            c[6] = 0;
             c[7] = 0;
             for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = ci;
             if (!p.mfma)                 // MFMA tiles weigh 1: filled in parallel below
@@ -562,7 +562,7 @@ __device__ void write_chunks(const MoeParams& p, const ExpertLds& ex, const int*
             c[3] = p.k2_shared;
             c[4] = u;
             c[5] = m;
-            c[6] = 0;
+            c[6] = p.k2_shared_d;
             c[7] = 0;
             for (int i = 0; i < m; ++i) p.unit_chunk[u + i] = base + j;
             if (!p.mfma)
@@ -782,6 +782,7 @@ constexpr int GEMV_PREP_WAVES = 4;
 struct GemvPrepLds {
     uint64_t tbl[9][EVAMX_MAX_EXPERTS];
     uint8_t k2[EVAMX_MAX_EXPERTS];
+    uint8_t k2d[EVAMX_MAX_EXPERTS];
     int sel[64];
     half_t rw[64];
 };
@@ -801,8 +802,10 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
     } else {
         const int nt = (GEMV_PREP_WAVES - p.T) * 64, i0 = t - p.T * 64;
         for (int i = i0; i < 9 * E; i += nt) sh.tbl[i / E][i % E] = (uint64_t)p.tables[(size_t)(i / E) * p.tbl_stride + i % E];
-        if (p.k2_per_expert)
-            for (int i = i0; i < E; i += nt) sh.k2[i] = p.k2_per_expert[i];
+        for (int i = i0; i < E; i += nt) {
+            sh.k2[i] = (uint8_t)k2_gu_of(p, i);
+            sh.k2d[i] = (uint8_t)k2_d_of(p, i);
+        }
     }
     if (!p.logits && t < slots) {
         const int64_t e = p.sel[t];
@@ -858,7 +861,7 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
             if (rs) p.runs[2 + __popcll(rmask & (le_mask >> 1)) ] = lane;
         }
         p.order[lane] = gs;
-        const int k2 = p.k2_per_expert ? (int)sh.k2[ge] : p.k2_uniform;
+        const int k2 = sh.k2[ge], k2d = sh.k2d[ge];
         SlotRec q;
         q.active = 1;
         q.shared = 0;
@@ -872,7 +875,7 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
         q.d_svh = sh.tbl[EVAMX_TBL_D_SVH][ge];
         p.srec[gs] = q;
         if (rs) {
-            if (!gemv_k2_supported(k2)) atomicOr(p.err, EVAMX_ERR_RATE);
+            if (!gemv_k2_supported(k2) || !gemv_k2_supported(k2d)) atomicOr(p.err, EVAMX_ERR_RATE);
             UnitRec r;
             r.e = ge;
             r.rows = rows;
@@ -880,7 +883,8 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
             r.ubase = ubase;
             r.s_gu = ks_of_chunk(kgu, m);
             r.s_d = ks_of_chunk(kd, m);
-            r.pad0[0] = r.pad0[1] = 0;
+            r.k2_d = k2d;
+            r.pad0 = 0;
 #pragma unroll
             for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = j < rows ? slot_run[j] : slot_run[0];
             r.tr[0] = sh.tbl[EVAMX_TBL_G_TRELLIS][ge];
@@ -918,7 +922,8 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
             r.ubase = routed_units;
             r.s_gu = ks_of_chunk(kgu, 1);
             r.s_d = ks_of_chunk(kd, 1);
-            r.pad0[0] = r.pad0[1] = 0;
+            r.k2_d = p.k2_shared_d;
+            r.pad0 = 0;
 #pragma unroll
             for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = slots + (j < p.T ? j : 0);
             r.tr[0] = (uint64_t)p.sh_ptr[EVAMX_TBL_G_TRELLIS];
@@ -1314,7 +1319,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     if (r >= ncg * S) return;
     const int cg = __builtin_amdgcn_readfirstlane(r / S), ks = __builtin_amdgcn_readfirstlane(r % S);
     const int rows = __builtin_amdgcn_readfirstlane(rp->rows);
-    const int k2 = __builtin_amdgcn_readfirstlane(rp->k2);
+    const int k2 = __builtin_amdgcn_readfirstlane(rp->k2_d);
     const int na = p.I / 128;
     const int c0 = na * ks / S, c1 = na * (ks + 1) / S;
     const uint32_t* trellis = (const uint32_t*)rp->tr[2];
@@ -1390,6 +1395,22 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     }
     const float L = p.limit;
     const int nslot = moe_nslot(p);
+    if (shared && a0 == 0 && p.sh_gate_w) {
+        // gated shared expert: the row's scale sigmoid(x . w), fp32 dot of the fp16 row
+        // (exl3_moe_coop_kernel.cuh:881-903), for the combine stage
+        const int row = s - p.T * p.topk;
+        const uint32_t* xw = (const uint32_t*)((const uint16_t*)p.x + (size_t)row * p.x_stride);
+        const uint32_t* ww = (const uint32_t*)p.sh_gate_w;
+        float d = 0.0f;
+        for (int i = lane; i < p.H / 2; i += 64) {
+            const uint32_t xv = xw[i];
+            const half2_t wv = __builtin_bit_cast(half2_t, ww[i]);
+            d = fmaf(x_elem(xv, 0, p.x_dtype), h2f(wv.x), d);
+            d = fmaf(x_elem(xv, 1, p.x_dtype), h2f(wv.y), d);
+        }
+        d = wave_sum(d);
+        if (lane == 0) p.gate_val[row] = 1.0f / (1.0f + __expf(-d));
+    }
     // all chunks' scales and partial sums first, so their loads are in flight together
     float g[CPW][2], u[CPW][2], gs[CPW][2], us[CPW][2], ds[CPW][2];
     const float* base[4 * CPW];
@@ -1586,6 +1607,12 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
         float v[2];
         sum_partials(p, sk, cg, lane, S, v);
         combine_item(shared, w, h2f(svh[col0]), h2f(svh[col1]), v, lane);
+        if (shared && p.sh_gate_w) {
+            // gated shared expert: gv * shared (exl3_moe_coop_kernel.cuh:942-948)
+            const float gv = p.gate_val[row];
+            v[0] = gv * v[0];
+            v[1] = gv * v[1];
+        }
         part[k][c0] = v[0];
         part[k][c1] = v[1];
         if (lane == 0) active[k] = 1;
@@ -1655,6 +1682,11 @@ __global__ __launch_bounds__(256) void moe_combine_rows_kernel(MoeParams p)
             const bool shared = b + j == p.topk;
             if (le[j] >= 0 || (shared && le[j] == -1)) {
                 combine_item(shared, w[j], sv[j][0], sv[j][1], v[j], lane);
+                if (shared && p.sh_gate_w) {
+                    const float gv = p.gate_val[row];
+                    v[j][0] = gv * v[j][0];
+                    v[j][1] = gv * v[j][1];
+                }
                 o0 = o0 + v[j][0];
                 o1 = o1 + v[j][1];
             }

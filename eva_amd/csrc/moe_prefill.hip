@@ -99,7 +99,7 @@ __device__ __forceinline__ void mfma_stage(const MoeParams& p, uint32_t (&lds)[M
     const int e = __builtin_amdgcn_readfirstlane(ch[0]);
     const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
     const int rows = __builtin_amdgcn_readfirstlane(ch[2]);
-    const int k2 = __builtin_amdgcn_readfirstlane(ch[3]);
+    const int k2 = __builtin_amdgcn_readfirstlane(ch[which == 0 ? 3 : 6]);    // gate/up or down rate
     const int* slot_of = p.order + begin;
     const int nslot = moe_nslot(p);
     const int trow = proj == 0 ? EVAMX_TBL_G_TRELLIS : proj == 1 ? EVAMX_TBL_U_TRELLIS : EVAMX_TBL_D_TRELLIS;

@@ -259,11 +259,22 @@ def _check_forward_args(s, device, x, tables, out, bits, k2_per_expert, logits, 
 
 
 def _moe_args(s, device, x, tables, out, limit, bits, k2_per_expert, logits, sel, weights, rw, score_fn, sel_bias,
-              route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events, residual, gate_w):
+              route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events, residual, gate_w,
+              bits_down=None, k2_down_per_expert=None, shared_bits_down=None, shared_gate_w=None):
     """The evamx_moe_args of one forward call (every tensor checked first), without the
     workspace; returns it with the ctypes array of shared pointers it refers to."""
     _check_forward_args(s, device, x, tables, out, bits, k2_per_expert, logits, sel, weights, rw, sel_bias,
                         shared_ptrs, shared_bits, events, residual, gate_w)
+    if k2_down_per_expert is not None:
+        _dev(k2_down_per_expert, "k2_down_per_expert", torch.uint8, 1)
+        if k2_down_per_expert.device != device or k2_down_per_expert.numel() != s.n_local:
+            raise ValueError(f"k2_down_per_expert must be a uint8 [{s.n_local}] tensor on {device}")
+    if shared_gate_w is not None:
+        _dev(shared_gate_w, "shared_gate_w", torch.float16, 1)
+        if shared_gate_w.device != device or shared_gate_w.numel() != s.hidden:
+            raise ValueError(f"shared_gate_w must be an fp16 [{s.hidden}] tensor on {device}")
+        if not s.has_shared:
+            raise ValueError("shared_gate_w needs a shared expert")
     a = MoeArgs()
     a.shape = s
     a.rows = x.shape[0]
@@ -301,6 +312,10 @@ def _moe_args(s, device, x, tables, out, limit, bits, k2_per_expert, logits, sel
         a.residual_stride = residual.stride(0)
     if events is not None:
         a.events = ctypes.cast(events, ctypes.c_void_p)
+    a.bits_down = float(bits_down) if bits_down is not None else 0.0
+    a.k2_down_per_expert = ptr(k2_down_per_expert)
+    a.shared_bits_down = float(shared_bits_down) if shared_bits_down is not None else 0.0
+    a.shared_gate_w = ptr(shared_gate_w)
     return a, keep
 
 
@@ -310,7 +325,9 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
                 weights: torch.Tensor | None = None, rw: torch.Tensor | None = None,
                 score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
                 shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1, max_expert: int = 0,
-                events=None, residual: torch.Tensor | None = None, gate_w: torch.Tensor | None = None):
+                events=None, residual: torch.Tensor | None = None, gate_w: torch.Tensor | None = None,
+                bits_down: float | None = None, k2_down_per_expert: torch.Tensor | None = None,
+                shared_bits_down: float | None = None, shared_gate_w: torch.Tensor | None = None):
     """One MoE layer: out[r] = sum over r's active slots (slot order) + shared expert.
 
     With ``logits`` the routing runs on the device and writes ``sel``/``weights``/``rw`` (all
@@ -322,10 +339,13 @@ def moe_forward(ws: MoeWorkspace, x: torch.Tensor, tables: torch.Tensor, out: to
     (may be ``x`` itself); ``out`` may then be None.
     ``gate_w``: optional fp32 ``[n_experts, H]`` router weight; the logits ``x @ gate_w.T`` are then
     computed on the device (instead of ``logits``) and routed with ``score_fn``/``sel_bias``.
+    ``bits_down`` / ``k2_down_per_expert`` / ``shared_bits_down``: the down projections' rate when
+    it differs from gate/up (the reference launcher's K_d). ``shared_gate_w``: fp16 ``[H]``; the
+    shared term is then scaled by sigmoid(x . shared_gate_w) per row.
     """
     a, keep = _moe_args(ws.shape, ws.buffer.device, x, tables, out, limit, bits, k2_per_expert, logits, sel, weights,
                         rw, score_fn, sel_bias, route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events,
-                        residual, gate_w)
+                        residual, gate_w, bits_down, k2_down_per_expert, shared_bits_down, shared_gate_w)
     a.workspace = ptr(ws.buffer)
     a.workspace_bytes = ws.buffer.numel()
     check(lib().evamx_moe_forward(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward")
@@ -340,7 +360,9 @@ def moe_forward_static(shape: MoeShape, x: torch.Tensor, tables: torch.Tensor, o
                        score_fn: str = "sigmoid", sel_bias: torch.Tensor | None = None, route_scale: float = 1.0,
                        shared_ptrs=None, shared_bits: float | None = None, min_expert: int = -1,
                        max_expert: int = 0, events=None, residual: torch.Tensor | None = None,
-                       gate_w: torch.Tensor | None = None):
+                       gate_w: torch.Tensor | None = None, bits_down: float | None = None,
+                       k2_down_per_expert: torch.Tensor | None = None, shared_bits_down: float | None = None,
+                       shared_gate_w: torch.Tensor | None = None):
     """``moe_forward`` without a workspace: evamx_moe_forward_static runs the layer on the
     library's fixed device scratch (64 MiB per GPU) and allocates nothing, for callers that
     cannot allocate (e.g. under graph capture). ``shape`` is the MoeShape a workspace would have
@@ -349,7 +371,7 @@ def moe_forward_static(shape: MoeShape, x: torch.Tensor, tables: torch.Tensor, o
         raise ValueError("x must be a device tensor")
     a, keep = _moe_args(shape, x.device, x, tables, out, limit, bits, k2_per_expert, logits, sel, weights, rw,
                         score_fn, sel_bias, route_scale, shared_ptrs, shared_bits, min_expert, max_expert, events,
-                        residual, gate_w)
+                        residual, gate_w, bits_down, k2_down_per_expert, shared_bits_down, shared_gate_w)
     check(lib().evamx_moe_forward_static(ctypes.byref(a), stream_handle(x.device)), "evamx_moe_forward_static")
     del keep
     return out

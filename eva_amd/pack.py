@@ -147,7 +147,7 @@ class ResidentLayer:
         dev_base = storage.data_ptr()
         recs = index.records[layer]
         rows = [[0] * len(recs) for _ in range(9)]
-        k2 = []
+        k2, k2d = [], []
         for e, r in enumerate(recs):
             for t, name in enumerate(TABLE_PROJ):
                 p = r.proj(name)
@@ -155,13 +155,18 @@ class ResidentLayer:
                 rows[3 * t + 0][e] = at + p.rel_trellis
                 rows[3 * t + 1][e] = at + p.rel_suh
                 rows[3 * t + 2][e] = at + p.rel_svh
-            rates = {r.proj(n).bits for n in PROJ_ORDER}
-            if len(rates) != 1:
-                raise ValueError(f"layer {layer} expert {e}: projections at different rates {sorted(rates)}")
-            k2.append(int(round(2 * rates.pop())))
+            # gate (w1) and up (w3) share one rate, as the reference's converter allocates them as
+            # one group; down (w2) may differ (the coop launcher's K_gu / K_d)
+            gu = {r.proj("w1").bits, r.proj("w3").bits}
+            if len(gu) != 1:
+                raise ValueError(f"layer {layer} expert {e}: gate and up at different rates {sorted(gu)}")
+            k2.append(int(round(2 * gu.pop())))
+            k2d.append(int(round(2 * r.proj("w2").bits)))
         self.table = torch.tensor(rows, dtype=torch.int64, device=storage.device)
         self.k2_host = tuple(k2)
         self.k2 = torch.tensor(k2, dtype=torch.uint8, device=storage.device)
+        self.k2_down_host = tuple(k2d)
+        self.k2_down = torch.tensor(k2d, dtype=torch.uint8, device=storage.device)
         r0 = recs[0]
         self.hidden = r0.proj("w1").in_features
         self.inter = r0.proj("w1").out_features

@@ -161,6 +161,17 @@ typedef struct evamx_moe_args {
      * logits == NULL, each row's logits are computed on the device in fp32 with a fixed
      * reduction order (independent of the batch) and routed as above. NULL for none. */
     const float* gate_w;
+    /* ABI 4. Optional rate of the down projections when it differs from gate/up (the reference
+     * launcher takes K_gu for gate and up and K_d for down, vendor/quant/exl3_moe_coop.cuh:80-83):
+     * a uniform bits_down, or per expert k2_down_per_expert (device [n_local], 2*bits); 0 / NULL:
+     * the gate/up rate. shared_bits_down likewise for the shared expert (0: shared_bits). */
+    float bits_down;
+    const uint8_t* k2_down_per_expert;
+    float shared_bits_down;
+    /* ABI 4. Optional gated shared expert (exl3_moe_coop_kernel.cuh:881-903,942-948): device fp16
+     * [hidden], 4-byte aligned; each row's shared term is scaled by sigmoid(x_row . shared_gate_w)
+     * (fp32 dot of the fp16 row) before it is added. NULL: ungated. */
+    const void* shared_gate_w;
 } evamx_moe_args;
 
 size_t evamx_moe_workspace_bytes(const evamx_moe_shape* shape);

@@ -213,18 +213,24 @@ def dequant_fast(trellis, K):
 class ExpertWeights:
     """One expert's three EXL3 projections (gate, up: [H -> I]; down: [I -> H]).
 
-    ``trellis`` int16 [in/16, out/16, T], ``suh`` fp16 [in], ``svh`` fp16 [out], rate ``K``.
-    Decoded fp16 matrices are cached on first use.
+    ``trellis`` int16 [in/16, out/16, T], ``suh`` fp16 [in], ``svh`` fp16 [out], rate ``K``
+    (gate and up; the reference launcher takes one rate for both, exl3_moe_coop.cuh:80-83) and
+    ``K_down`` for the down projection (default: ``K``). Decoded fp16 matrices are cached on
+    first use.
     """
 
-    def __init__(self, g, u, d, K):
+    def __init__(self, g, u, d, K, K_down=None):
         self.parts = {"g": g, "u": u, "d": d}     # each (trellis, suh, svh)
         self.K = float(K)
+        self.K_down = float(K if K_down is None else K_down)
         self._dec = {}
+
+    def rate(self, p):
+        return self.K_down if p == "d" else self.K
 
     def W(self, p):
         if p not in self._dec:
-            self._dec[p] = dequant_fast(self.parts[p][0], self.K)
+            self._dec[p] = dequant_fast(self.parts[p][0], self.rate(p))
         return self._dec[p]
 
     def suh(self, p):
@@ -341,25 +347,39 @@ def swiglu(gate, up, limit):
 
 def shared_expert(x_fp16, ew: ExpertWeights, limit):
     """model.py:450-452: gate/up EXL3 linears, fp32 swiglu, fp16, down linear, fp32."""
-    gate = exl3_linear(x_fp16, *ew.parts["g"], ew.K, W=ew.W("g"))
-    up = exl3_linear(x_fp16, *ew.parts["u"], ew.K, W=ew.W("u"))
+    gate = exl3_linear(x_fp16, *ew.parts["g"], ew.rate("g"), W=ew.W("g"))
+    up = exl3_linear(x_fp16, *ew.parts["u"], ew.rate("u"), W=ew.W("u"))
     mid = swiglu(gate, up, limit).astype(np.float16)
-    return _f32(exl3_linear(mid, *ew.parts["d"], ew.K, W=ew.W("d")))
+    return _f32(exl3_linear(mid, *ew.parts["d"], ew.rate("d"), W=ew.W("d")))
+
+
+def shared_gate(x_fp16, gate_w_fp16):
+    """exl3_moe_coop_kernel.cuh:881-903: the gated shared expert's per-row scale
+    sigmoid(x_row . w), the dot in fp32 over fp16 values (the kernel's reduction order and
+    __expf are not reproduced: held to tolerance)."""
+    x = _f32(np.asarray(x_fp16, dtype=np.float16)).astype(np.float64)
+    w = _f32(np.asarray(gate_w_fp16, dtype=np.float16)).astype(np.float64)
+    t = x @ w
+    return (1.0 / (1.0 + np.exp(-t))).astype(np.float32)
 
 
 def moe_layer(x, logits, experts, shared, topk, limit, score_fn="sigmoid", sel_bias=None,
-              route_scale=1.0):
+              route_scale=1.0, shared_gate_w=None):
     """Block.experts (model.py:454-499) for one layer, routed from given logits.
 
     Returns (y fp32 [T,H] = routed + shared, idx, w fp32, rw fp16). The caller casts y to
-    the activation dtype (model.py:499).
+    the activation dtype (model.py:499). With ``shared_gate_w`` the shared term is
+    sigmoid(x . w) * shared (exl3_moe_coop_kernel.cuh:942-948).
     """
     xh = np.asarray(x, dtype=np.float32).astype(np.float16)
     idx, w = route(logits, topk, score_fn, sel_bias, route_scale)
     rw = w.astype(np.float16)
     y = moe_routed(xh, idx, rw, experts, limit)
     if shared is not None:
-        y = (y + shared_expert(xh, shared, limit)).astype(np.float32)
+        sh = shared_expert(xh, shared, limit)
+        if shared_gate_w is not None:
+            sh = (shared_gate(xh, shared_gate_w)[:, None] * sh).astype(np.float32)
+        y = (y + sh).astype(np.float32)
     return y, idx, w, rw
 
 

@@ -27,11 +27,13 @@ def projection(rng, n_in, n_out, K, svh_scale=1.0):
     return trellis, suh, svh
 
 
-def expert(rng, hidden, inter, K, svh_scale=1.0):
+def expert(rng, hidden, inter, K, svh_scale=1.0, K_down=None):
+    """Gate and up at rate K, down at K_down (default K)."""
+    Kd = K if K_down is None else K_down
     g = projection(rng, hidden, inter, K, svh_scale)
     u = projection(rng, hidden, inter, K, svh_scale)
-    d = projection(rng, inter, hidden, K, svh_scale)
-    return ExpertWeights(g, u, d, K)
+    d = projection(rng, inter, hidden, Kd, svh_scale)
+    return ExpertWeights(g, u, d, K, Kd)
 
 
 def activations_bf16(rng, t, hidden):

@@ -32,6 +32,7 @@ class DeviceExperts:
         table = np.array(self.rows, dtype=np.int64).T.copy()     # [9, n]
         self.table = torch.from_numpy(table).to(device)
         self.k2 = torch.tensor([int(round(2 * ew.K)) for ew in experts], dtype=torch.uint8, device=device)
+        self.k2_down = torch.tensor([int(round(2 * ew.K_down)) for ew in experts], dtype=torch.uint8, device=device)
 
     def ptrs(self, i):
         return self.rows[i]

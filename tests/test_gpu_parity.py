@@ -108,6 +108,69 @@ def test_exl3_linear_mfma_path(dev, K, rows):
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
 
 
+def _run_layer(ops, dev, x, logits, de, ds, H, I, E, topk, rows, limit, **kw):
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    sel = torch.empty(rows, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(rows, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), de.table, out, limit=limit, logits=to_dev(logits, dev),
+                    sel=sel, weights=w, shared_ptrs=ds.ptrs(0), **kw)
+    torch.cuda.synchronize()
+    assert int(ws.flags().cpu()[0]) == 0
+    return out.cpu().numpy(), sel.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5, 40])
+def test_moe_layer_down_rate_differs(dev, rows):
+    """Gate/up and down at different rates (the reference launcher's K_gu and K_d,
+    exl3_moe_coop.cuh:80-83): per-expert down-rate tables, a uniform down rate, and a shared
+    expert whose down rate differs; through the decode GEMV (1-2 rows), the 16-row MFMA tiles
+    (5) and the 64-row tiles (40)."""
+    ops = _ops()
+    H, I, E, topk, limit = 512, 256, 16, 4, 10.0
+    rng = np.random.default_rng(300 + rows)
+    pairs = [(4, 3), (3, 2), (2, 4), (2.5, 3.5), (4, 5), (1.5, 2), (3.5, 1.5), (5, 2.5)]
+    experts = [synth.expert(rng, H, I, pairs[e % len(pairs)][0], svh_scale=1 / np.sqrt(H),
+                            K_down=pairs[e % len(pairs)][1]) for e in range(E)]
+    shared = synth.expert(rng, H, I, 4, svh_scale=1 / np.sqrt(H), K_down=3)
+    x = synth.activations_bf16(rng, rows, H)
+    logits = synth.logits_plain(rng, rows, E)
+    ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+    de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+    y, sel = _run_layer(ops, dev, x, logits, de, ds, H, I, E, topk, rows, limit, k2_per_expert=de.k2,
+                        k2_down_per_expert=de.k2_down, shared_bits=4.0, shared_bits_down=3.0)
+    assert np.array_equal(sel, ridx)
+    assert rel_err_rows(y, ref) < TOL
+    # uniform rates: gate/up 4, down 2.5
+    experts_u = [synth.expert(rng, H, I, 4, svh_scale=1 / np.sqrt(H), K_down=2.5) for _ in range(E)]
+    ref_u, _, _, _ = coop.moe_layer(x, logits, experts_u, shared, topk, limit)
+    de_u = DeviceExperts(experts_u, dev)
+    y_u, _ = _run_layer(ops, dev, x, logits, de_u, ds, H, I, E, topk, rows, limit, bits=4.0, bits_down=2.5,
+                        shared_bits=4.0, shared_bits_down=3.0)
+    assert rel_err_rows(y_u, ref_u) < TOL
+
+
+@pytest.mark.parametrize("rows", [1, 2, 8, 40])
+def test_moe_layer_gated_shared_expert(dev, rows):
+    """Gated shared expert (exl3_moe_coop_kernel.cuh:881-903,942-948): the shared term scaled by
+    sigmoid(x . w) per row, against the oracle; the gate visibly changes the output."""
+    ops = _ops()
+    H, I, E, topk, limit = 512, 256, 16, 4, 10.0
+    rng = np.random.default_rng(400 + rows)
+    experts, shared = _layer_case(rng, H, I, E, 4, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, rows, H)
+    logits = synth.logits_plain(rng, rows, E)
+    gw = (rng.standard_normal(H) * 0.08).astype(np.float16)
+    ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit, shared_gate_w=gw)
+    ungated, _, _, _ = coop.moe_layer(x, logits, experts, shared, topk, limit)
+    assert rel_err_rows(ungated, ref) > 5 * TOL
+    de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+    y, sel = _run_layer(ops, dev, x, logits, de, ds, H, I, E, topk, rows, limit, bits=4.0, shared_bits=4.0,
+                        shared_gate_w=to_dev(gw, dev))
+    assert np.array_equal(sel, ridx)
+    assert rel_err_rows(y, ref) < TOL
+
+
 def _layer_case(rng, H, I, E, K, svh_scale, rates=None):
     experts = []
     for e in range(E):

@@ -176,6 +176,48 @@ def test_coop_expert_against_dense_formula():
     assert coop.rel_err_rows(got, ref) < 5e-3
 
 
+def test_expert_with_its_own_down_rate():
+    """Gate/up at 4 bpw, down at 3 bpw (the launcher's K_gu / K_d, exl3_moe_coop.cuh:80-83):
+    each projection decodes at its own rate, and the expert matches the dense formula."""
+    rng = np.random.default_rng(21)
+    ew = synth.expert(rng, 256, 128, 4, svh_scale=1.0 / 16, K_down=3)
+    assert ew.parts["g"][0].shape[-1] == 64 and ew.parts["d"][0].shape[-1] == 48
+    assert np.array_equal(ew.W("d").view(np.uint16), exl3.dequant(ew.parts["d"][0], 3).view(np.uint16))
+    assert np.array_equal(ew.W("g").view(np.uint16), exl3.dequant(ew.parts["g"][0], 4).view(np.uint16))
+    x = (rng.standard_normal((2, 256)) * 2).astype(np.float16)
+    assert coop.rel_err_rows(coop.coop_expert(x, ew, 10.0), _dense_expert(x, ew, 10.0)) < 5e-3
+    assert coop.rel_err_rows(coop.shared_expert(x, ew, 10.0), _dense_expert(x, ew, 10.0, clamp_after=False)) < 1e-2
+
+
+def test_shared_gate_closed_forms():
+    """Gated shared expert (exl3_moe_coop_kernel.cuh:881-903,942-948): y = routed +
+    sigmoid(x . w) * shared. w = 0 gives exactly half the shared term; a large positive dot
+    gives the ungated layer, a large negative one the routed part alone."""
+    rng = np.random.default_rng(22)
+    H, I, E, topk = 256, 128, 4, 2
+    experts = [_small_expert(rng, H, I) for _ in range(E)]
+    shared = _small_expert(rng, H, I)
+    x = synth.activations_bf16(rng, 3, H)
+    logits = synth.logits_plain(rng, 3, E)
+    y0, idx, _, rw = coop.moe_layer(x, logits, experts, shared, topk, 10.0)
+    routed = coop.moe_routed(np.asarray(x, np.float32).astype(np.float16), idx, rw, experts, 10.0)
+    sh = y0 - routed
+    yh, *_ = coop.moe_layer(x, logits, experts, shared, topk, 10.0, shared_gate_w=np.zeros(H, np.float16))
+    assert coop.rel_err_rows(yh - routed, 0.5 * sh) < 1e-5
+    w = (rng.standard_normal(H) * 0.05).astype(np.float16)
+    g = coop.shared_gate(np.asarray(x, np.float32).astype(np.float16), w)
+    assert g.shape == (3,) and np.all((g > 0.01) & (g < 0.99))
+    t = np.asarray(x, np.float32).astype(np.float16).astype(np.float64) @ w.astype(np.float64)
+    assert np.allclose(g, 1 / (1 + np.exp(-t)), rtol=1e-6)
+    yg, *_ = coop.moe_layer(x, logits, experts, shared, topk, 10.0, shared_gate_w=w)
+    assert coop.rel_err_rows(yg - routed, g[:, None] * sh) < 1e-5
+    big = np.full(H, 60.0, np.float16) * np.sign(np.asarray(x, np.float32)[0]).astype(np.float16)
+    yb, *_ = coop.moe_layer(x[:1], logits[:1], experts, shared, topk, 10.0, shared_gate_w=big)
+    assert coop.rel_err_rows(yb, y0[:1]) < 1e-6
+    yn, *_ = coop.moe_layer(x[:1], logits[:1], experts, shared, topk, 10.0, shared_gate_w=-big)
+    assert coop.rel_err_rows(yn, routed[:1]) < 1e-6
+
+
 def test_activation_clamp_semantics():
     g = np.array([30.0, -30.0, 12.0, 0.5], np.float32)
     u = np.array([20.0, 3.0, -15.0, 0.25], np.float32)
