@@ -162,13 +162,30 @@ __device__ __forceinline__ uint64_t pack_key(float k, int e)
     return ((uint64_t)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
-template <int M>
-__device__ __forceinline__ uint64_t max_x(uint64_t v, int lane)
+// Maximum of one 32-bit value per lane over the wave, in every lane: quad maxima by two quad
+// permutations, row maxima by rotations of 4 and 8 within the row, then across rows.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v, int lane)
 {
-    const uint32_t lo = xor_lane<M>((uint32_t)v, lane);
-    const uint32_t hi = xor_lane<M>((uint32_t)(v >> 32), lane);
-    const uint64_t p = ((uint64_t)hi << 32) | lo;
-    return p > v ? p : v;
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, false));    // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, false));    // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xf, 0xf, false));   // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false));   // row_ror:8
+    v = max(v, xor_lane<16>(v, lane));
+    v = max(v, xor_lane<32>(v, lane));
+    return v;
+}
+
+// The lane holding the wave's largest key (one head key per lane): the largest high word, and
+// among lanes tied on it the largest low word (the lowest expert index).
+__device__ __forceinline__ int wave_argmax_key(uint64_t k, int lane)
+{
+    const uint32_t hk = (uint32_t)(k >> 32);
+    const uint32_t m = __builtin_amdgcn_readfirstlane(wave_max_u32(hk, lane));
+    const uint64_t tie = __ballot(hk == m);
+    if (__builtin_amdgcn_readfirstlane(__popcll(tie)) == 1) return __ffsll((long long)tie) - 1;
+    const uint32_t lo = hk == m ? (uint32_t)k : 0u;
+    const uint32_t ml = __builtin_amdgcn_readfirstlane(wave_max_u32(lo, lane));
+    return __ffsll((long long)__ballot(hk == m && (uint32_t)k == ml)) - 1;
 }
 
 // Compare-exchange of two (key, logit) entries into descending key order.
@@ -222,16 +239,10 @@ __device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, h
     float my_z = 0.0f;
     int my_id = 0;
     for (int j = 0; j < p.topk; ++j) {
-        uint64_t best = key[0];
-        best = max_x<1>(best, lane);
-        best = max_x<2>(best, lane);
-        best = max_x<4>(best, lane);
-        best = max_x<8>(best, lane);
-        best = max_x<16>(best, lane);
-        best = max_x<32>(best, lane);
-        const int bi = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)best));
-        const float zb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, zr[0]), bi & 63));
-        if (lane == (bi & 63)) {
+        const int wl = __builtin_amdgcn_readfirstlane(wave_argmax_key(key[0], lane));
+        const int bi = (int)(0xffffffffu - (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wl));
+        const float zb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, zr[0]), wl));
+        if (lane == wl) {
 #pragma unroll
             for (int i = 0; i + 1 < NPER; ++i) {
                 key[i] = key[i + 1];
