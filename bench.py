@@ -561,7 +561,9 @@ def run_layer(torch, args):
 
     # Per-kernel durations on the launch stream (eager pass, events between the launches).
     n_ev = 16 if prefill else 64
-    kt = kernel_times(torch, stream, step, n_ev, skip=2 if prefill else 8)
+    # one-token calls route inside the gate/up launch: their prepare stage has no kernel
+    kt = kernel_times(torch, stream, step, n_ev, skip=2 if prefill else 8,
+                      kernelless=("moe_prepare",) if T == 1 else ())
     gu_bytes_launch = sum(layers.gate_up_bytes(i % args.layers, touched[i % n_draws]) for i in range(n_ev)) / n_ev
     roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, args.bits))
     if prefill:
@@ -594,6 +596,8 @@ def run_layer(torch, args):
         "kernel_us": {k: round(v, 3) for k, v in kt.items()},
         "roofline": roofline,
     }
+    if T == 1:
+        result["kernel_us_note"] = "1 token: routing runs inside moe_gate_up (no prepare launch)"
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         what = f"step 0 of the timed sequence (layer 0, routing draw 0){'' if T == 1 else f', first token of {T}'}"
@@ -680,6 +684,8 @@ def run_stack(torch, args):
         "kernel_us": {k: round(v, 3) for k, v in kt.items()},
         "roofline": roofline,
     }
+    if T == 1:
+        result["kernel_us_note"] = "1 token: routing runs inside moe_gate_up (no prepare launch)"
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(torch, layers, 0, h0, logits[0], 1, 10.0,
@@ -850,10 +856,11 @@ def measured_traffic(tokens, bits):
     return int(m.group(1)) if m else None
 
 
-def kernel_times(torch, stream, step, n, skip):
+def kernel_times(torch, stream, step, n, skip, kernelless=()):
     """Average duration of each of the five stages, from the start timestamp of a stage's first
     kernel to the end timestamp of its last (events taken by the kernel launches themselves on
-    the launch stream; eager calls step(i, events))."""
+    the launch stream; eager calls step(i, events)). Stages in ``kernelless`` run inside another
+    stage's launch in these calls and record no events (evamx_moe_args.events): reported as 0."""
     names = ["moe_prepare", "moe_gate_up", "moe_act", "moe_down", "moe_combine"]
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(10)] for _ in range(n)]
     for row in evs:
@@ -871,7 +878,7 @@ def kernel_times(torch, stream, step, n, skip):
     for i in range(skip, n):
         for k in range(5):
             acc[k] += evs[i][2 * k].elapsed_time(evs[i][2 * k + 1])
-    return {names[k]: acc[k] * 1e3 / (n - skip) for k in range(5)}
+    return {names[k]: 0.0 if names[k] in kernelless else acc[k] * 1e3 / (n - skip) for k in range(5)}
 
 
 if __name__ == "__main__":

@@ -200,8 +200,9 @@ __device__ __forceinline__ void ce_desc(uint64_t& ka, float& za, uint64_t& kb, f
     za = z;
 }
 
+// Top-k of row r: lane j < topk ends with winner j's expert index and routing weight.
 template <int NPER>
-__device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
+__device__ __forceinline__ void route_winners(const MoeParams& p, int r, int lane, int& id, float& w)
 {
     static_assert(NPER == 4 || NPER == 8, "4 or 8 keys per lane");
     const float* z = p.logits + (size_t)r * p.n_logits;
@@ -257,8 +258,17 @@ __device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, h
     float tot = 0.0f;
     for (int j = 0; j < p.topk; ++j)
         tot = tot + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), j));
+    id = my_id;
+    w = lane < p.topk ? route_weight(sc, tot, p.route_scale) : 0.0f;
+}
+
+template <int NPER>
+__device__ void route_token_n(const MoeParams& p, int r, int lane, int* sel_o, half_t* rw_o, bool publish)
+{
+    int my_id;
+    float w;
+    route_winners<NPER>(p, r, lane, my_id, w);
     if (lane < p.topk) {
-        const float w = route_weight(sc, tot, p.route_scale);
         const int s = r * p.topk + lane;
         if (sel_o) sel_o[s] = my_id;
         if (rw_o) rw_o[s] = f2h(w);
@@ -276,6 +286,12 @@ __device__ __forceinline__ void route_token(const MoeParams& p, int r, int lane,
 {
     if (p.n_logits <= 256) route_token_n<4>(p, r, lane, sel_o, rw_o, publish);
     else route_token_n<EVAMX_MAX_EXPERTS / 64>(p, r, lane, sel_o, rw_o, publish);
+}
+
+__device__ __forceinline__ void route_lanes(const MoeParams& p, int r, int lane, int& id, float& w)
+{
+    if (p.n_logits <= 256) route_winners<4>(p, r, lane, id, w);
+    else route_winners<EVAMX_MAX_EXPERTS / 64>(p, r, lane, id, w);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -617,6 +633,14 @@ __device__ __forceinline__ float x_elem(uint32_t w, int hi, int dtype)
     return x_fp16_value((uint16_t)(hi ? w >> 16 : w), dtype);
 }
 
+// A wave-uniform 64-bit value through two 32-bit readfirstlanes (the builtin takes an int).
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
 // Chunks [c0, c1) of grouped slot s (routed slot < T*topk with local expert e, or shared row).
 __device__ void rotate_chunks(const MoeParams& p, int s, int e, int proj, int c0, int c1, int lane)
 {
@@ -624,7 +648,12 @@ __device__ void rotate_chunks(const MoeParams& p, int s, int e, int proj, int c0
     const bool shared = s >= slots;
     const int row = shared ? s - slots : s / p.topk;
     const int trow = proj == 0 ? EVAMX_TBL_G_SUH : EVAMX_TBL_U_SUH;
-    const half_t* suh = shared ? (const half_t*)p.sh_ptr[trow] : (const half_t*)p.tables[(size_t)trow * p.tbl_stride + e];
+    // the shared pointer selected by value: a select of addresses into the kernel argument (an
+    // indexed access) puts the whole argument in scratch memory
+    const uint64_t sg = uniform_u64((uint64_t)p.sh_ptr[EVAMX_TBL_G_SUH]);
+    const uint64_t su = uniform_u64((uint64_t)p.sh_ptr[EVAMX_TBL_U_SUH]);
+    const half_t* suh = shared ? (const half_t*)(proj == 0 ? sg : su)
+                               : (const half_t*)p.tables[(size_t)trow * p.tbl_stride + e];
     const uint32_t* xw = (const uint32_t*)((const uint16_t*)p.x + (size_t)row * p.x_stride) + lane;
     const uint32_t* sw = (const uint32_t*)suh + lane;
     uint32_t* dst = (uint32_t*)(p.xr + ((size_t)proj * p.nslot_max + s) * p.H) + lane;
@@ -1167,15 +1196,10 @@ struct RotStageGroup {
 // streamed; writes the fp32 partials of the rows.
 template <int K2, int TM, bool GROUP>
 __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
-                                                 const int* slot, int tm, int cg, int c0, int c1, float* part,
+                                                 const int (&so)[TM], int tm, int cg, int c0, int c1, float* part,
                                                  uint32_t* lds, float* lsums)
 {
     const int lane = threadIdx.x & 63;
-    // the record is not written during this kernel: scalar loads of its slots
-    const __attribute__((address_space(4))) int* sl = (const __attribute__((address_space(4))) int*)slot;
-    int so[TM];
-#pragma unroll
-    for (int m = 0; m < TM; ++m) so[m] = __builtin_amdgcn_readfirstlane(sl[m < tm ? m : 0]);
     float acc[TM][2], xs[TM];
 #pragma unroll
     for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = xs[m] = 0.0f;
@@ -1223,25 +1247,45 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
     }
 }
 
+// Slots slot[0..tm) of a unit record (entries past tm repeat slot[0]); the record is not written
+// during the GEMV launch, so these are scalar loads.
+template <int TM>
+__device__ __forceinline__ void record_slots(const int* slot, int tm, int (&so)[TM])
+{
+    const __attribute__((address_space(4))) int* sl = (const __attribute__((address_space(4))) int*)slot;
+#pragma unroll
+    for (int m = 0; m < TM; ++m) so[m] = __builtin_amdgcn_readfirstlane(sl[m < tm ? m : 0]);
+}
+
+template <int K2, int TM, bool GROUP>
+__device__ __forceinline__ void gate_up_rot_rec(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
+                                                const int* slot, int tm, int cg, int c0, int c1, float* part,
+                                                uint32_t* lds, float* lsums)
+{
+    int so[TM];
+    record_slots<TM>(slot, tm, so);
+    gate_up_rot_rows<K2, TM, GROUP>(p, trellis, suh, so, tm, cg, c0, c1, part, lds, lsums);
+}
+
 template <int K2, int TMAX, bool GROUP>
 __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                  const int* slot, int rows, int cg, int c0, int c1, float* part,
                                                  uint32_t* lds, float* lsums)
 {
     if (rows <= TMAX) {                 // the common case, straight-line
-        if constexpr (TMAX == 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
-        else if (rows <= 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
-        else gate_up_rot_rows<K2, 2, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
+        if constexpr (TMAX == 1) gate_up_rot_rec<K2, 1, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
+        else if (rows <= 1) gate_up_rot_rec<K2, 1, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
+        else gate_up_rot_rec<K2, 2, GROUP>(p, trellis, suh, slot, rows, cg, c0, c1, part, lds, lsums);
         return;
     }
     // a chunk of more than TMAX rows (given routes that repeat an expert) runs TMAX rows at a time
     for (int r0 = 0; r0 < rows; r0 += TMAX) {
         const int tr = rows - r0 < TMAX ? rows - r0 : TMAX;
-        if constexpr (TMAX == 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+        if constexpr (TMAX == 1) gate_up_rot_rec<K2, 1, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
         else {
             static_assert(TMAX == 2, "decode path rows: 1 or 2");
-            if (tr <= 1) gate_up_rot_rows<K2, 1, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
-            else gate_up_rot_rows<K2, 2, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+            if (tr <= 1) gate_up_rot_rec<K2, 1, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+            else gate_up_rot_rec<K2, 2, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
         }
         if constexpr (GROUP) __syncthreads();      // this pass's LDS reads before the next pass's writes
         else wave_lds_fence();
@@ -1307,6 +1351,198 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
                 dst[lane_col(lane, 0)] = 0.0f;
                 dst[lane_col(lane, 1)] = 0.0f;
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// One-row calls route inside the gate/up launch (no prepare launch). Units are the routed slots
+// in slot order, then the shared expert: unit j is slot j, so a gate/up wave knows its slot from
+// its unit alone. Each routed wave routes the token itself (every wave computes the same routes)
+// and reads its expert's pointers; the shared expert's waves start streaming at once. The grid's
+// extra last workgroup publishes what moe_prepare_gemv_kernel publishes for the later stages and
+// the caller: routes, local experts, the run table and order, the unit and slot records, meta.
+
+// The expert and fp16 routing weight of slot j of the one-row call, in lane j < topk.
+__device__ __forceinline__ void slot_routes1(const MoeParams& p, int lane, int& id, half_t& rw, float& w32)
+{
+    id = -1;
+    rw = f2h(0.0f);
+    w32 = 0.0f;
+    if (p.logits) {
+        route_lanes(p, 0, lane, id, w32);
+        rw = f2h(w32);
+    } else if (lane < p.topk) {
+        const int64_t e = p.sel[lane];
+        // indices outside the int range are outside any table: keep them out of range
+        id = (e >= 0 && e < 0x7fffffff) ? (int)e : -1;
+        rw = p.weights ? f2h(p.weights[lane]) : p.rw16[lane];
+    }
+}
+
+__device__ __forceinline__ void publish_routes1(const MoeParams& p, int lane)
+{
+    const int topk = p.topk;                       // slots 0..topk-1; the shared row is slot topk
+    if (p.runs) {
+        const int table_len = 2 + 2 * p.slots_max + 1;
+        for (int i = lane; i < table_len; i += 64) p.runs[i] = 0;
+    }
+    int id;
+    half_t rw;
+    float w32;
+    slot_routes1(p, lane, id, rw, w32);
+    int e = -1;
+    if (lane < topk) {
+        if (p.logits) {
+            p.sel[lane] = id;
+            p.weights[lane] = w32;
+            p.rw16[lane] = rw;
+        } else if (p.weights) {
+            p.rw16[lane] = rw;
+        }
+        e = slot_local(p, id, rw, true);
+        p.local[lane] = e;
+    }
+    // unit and slot records: lane j < topk for slot j, lane topk for the shared expert
+    const int sgu = ks_of_chunk(ks_gate_up(p, p.units_max), 1), sd = ks_of_chunk(ks_down(p, p.units_max), 1);
+    const bool sh_lane = p.has_shared && lane == topk;
+    if (lane < topk || sh_lane) {
+        SlotRec q = {};
+        UnitRec r = {};
+        r.e = EVAMX_NO_UNIT;
+        if (sh_lane || e >= 0) {
+            const int ex = sh_lane ? -1 : e;
+            auto ptr = [&](int row) -> uint64_t {
+                return sh_lane ? (uint64_t)p.sh_ptr[row] : (uint64_t)p.tables[(size_t)row * p.tbl_stride + e];
+            };
+            const int k2 = k2_gu_of(p, ex), k2d = k2_d_of(p, ex);
+            if (!gemv_k2_supported(k2) || !gemv_k2_supported(k2d)) atomicOr(p.err, EVAMX_ERR_RATE);
+            q.active = 1;
+            q.shared = sh_lane ? 1 : 0;
+            q.s_gu = sgu;
+            q.s_d = sd;
+            q.w = sh_lane ? 1.0f : h2f(rw);
+            q.g_svh = ptr(EVAMX_TBL_G_SVH);
+            q.u_svh = ptr(EVAMX_TBL_U_SVH);
+            q.d_suh = ptr(EVAMX_TBL_D_SUH);
+            q.d_svh = ptr(EVAMX_TBL_D_SVH);
+            r.e = ex;
+            r.rows = 1;
+            r.k2 = k2;
+            r.ubase = lane;
+            r.s_gu = sgu;
+            r.s_d = sd;
+            r.k2_d = k2d;
+#pragma unroll
+            for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = lane;
+            r.tr[0] = ptr(EVAMX_TBL_G_TRELLIS);
+            r.tr[1] = ptr(EVAMX_TBL_U_TRELLIS);
+            r.tr[2] = ptr(EVAMX_TBL_D_TRELLIS);
+            r.suh[0] = ptr(EVAMX_TBL_G_SUH);
+            r.suh[1] = ptr(EVAMX_TBL_U_SUH);
+        }
+        p.srec[lane] = q;
+        p.urec[lane] = r;
+    }
+    // the run table's zeros (other lanes) complete before its entries are written
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // stable grouping by (expert, slot), as moe_prepare_gemv_kernel
+    const uint32_t key = wave_sort_asc(e >= 0 ? ((uint32_t)e << 6) | (uint32_t)lane : 0xffffffffu, lane);
+    const bool act = key != 0xffffffffu;
+    const int ge = (int)(key >> 6), gs = (int)(key & 63);
+    const int n_active = __popcll(__ballot(act));
+    const int prev_e = __shfl_up(ge, 1, WAVE);
+    const uint64_t heads = __ballot(act && (lane == 0 || prev_e != ge));
+    const uint64_t le_mask = lane == 63 ? ~0ull : ((2ull << lane) - 1);
+    const int first = 63 - __clzll(heads & le_mask);
+    const bool rs = act && ((lane - first) % EVAMX_CHUNK) == 0;
+    const uint64_t rmask = __ballot(rs);
+    const int n_runs = __popcll(rmask);
+    if (act) {
+        if (p.runs) {
+            p.runs[2 + p.slots_max + 1 + lane] = gs;
+            if (rs) p.runs[2 + __popcll(rmask & (le_mask >> 1))] = lane;
+        }
+        p.order[lane] = gs;
+    }
+    if (lane == 0) {
+        if (p.has_shared) p.order[n_active] = topk;
+        if (p.runs) {
+            p.runs[0] = n_runs;
+            p.runs[1] = 0;
+            p.runs[2 + n_runs] = n_active;
+        }
+        p.meta[0] = n_runs + (p.has_shared ? 1 : 0);
+        p.meta[1] = n_active;
+        p.meta[2] = topk + (p.has_shared ? 1 : 0);
+        p.meta[3] = 0;
+    }
+}
+
+template <bool GROUP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_route1_kernel(MoeParams p)
+{
+    __shared__ uint32_t xl[GROUP ? 1 : 4][ROT_CW * 64];
+    __shared__ float xsums[ROT_CW];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (blockIdx.x == gridDim.x - 1) {
+        if (wave == 0) publish_routes1(p, lane);
+        return;
+    }
+    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int ncg = p.I / 128;
+    const int S = ks_of_chunk(ks_gate_up(p, p.units_max), 1);
+    const int per_unit = 2 * ncg * S;
+    const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
+    if (u >= p.units_max) return;
+    const int r = wid - u * per_unit;
+    int cg, proj, ks;
+    if constexpr (GROUP) {
+        cg = __builtin_amdgcn_readfirstlane(r % ncg);
+        const int pk = r / ncg;
+        proj = __builtin_amdgcn_readfirstlane(pk / S);
+        ks = __builtin_amdgcn_readfirstlane(pk % S);
+    } else {
+        cg = __builtin_amdgcn_readfirstlane(r / (2 * S));
+        const int rem = r % (2 * S);
+        proj = __builtin_amdgcn_readfirstlane(rem / S);
+        ks = __builtin_amdgcn_readfirstlane(rem % S);
+    }
+    int e = -1;                                   // the shared expert's unit (u == topk)
+    if (u < p.topk) {
+        int id;
+        half_t rw;
+        float w32;
+        slot_routes1(p, lane, id, rw, w32);
+        id = __builtin_amdgcn_readlane(id, u);
+        const half_t rwu = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_readlane((int)__builtin_bit_cast(uint16_t, rw), u));
+        e = __builtin_amdgcn_readfirstlane(slot_local(p, id, rwu, false));
+        if (e < 0) return;                        // inactive slot: no partials are read
+    }
+    const int k2 = __builtin_amdgcn_readfirstlane(k2_gu_of(p, e));
+    // constant table rows (a row index that depends on proj would put the kernel argument's
+    // shared-pointer array in scratch memory to index it)
+    const uint32_t* trellis = (const uint32_t*)(proj == 0 ? expert_ptr(p, e, EVAMX_TBL_G_TRELLIS)
+                                                          : expert_ptr(p, e, EVAMX_TBL_U_TRELLIS));
+    const half_t* suh = (const half_t*)(proj == 0 ? expert_ptr(p, e, EVAMX_TBL_G_SUH) : expert_ptr(p, e, EVAMX_TBL_U_SUH));
+    const int nch = p.H / 128;
+    const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
+    float* part = p.part_gu + ((size_t)ks * 2 + proj) * moe_nslot(p) * p.I;
+    uint32_t* lds = xl[GROUP ? 0 : wave];
+    const int so[1] = {u};                        // unit u is slot u (the shared row: slot topk)
+    switch (k2) {
+        case 3: gate_up_rot_rows<3, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        case 4: gate_up_rot_rows<4, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        case 5: gate_up_rot_rows<5, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        case 6: gate_up_rot_rows<6, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        case 7: gate_up_rot_rows<7, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        case 8: gate_up_rot_rows<8, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        case 10: gate_up_rot_rows<10, 1, GROUP>(p, trellis, suh, so, 1, cg, c0, c1, part, lds, xsums); break;
+        default: {
+            // unsupported rate (flagged by the publishing wave): zero partials
+            float* dst = part + (size_t)u * p.I + cg * 128;
+            dst[lane_col(lane, 0)] = 0.0f;
+            dst[lane_col(lane, 1)] = 0.0f;
         }
     }
 }
@@ -1740,13 +1976,18 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
     // most one unit per slot plus the shared expert's one (its rows fit one chunk)
     p.units_max = p.T * p.topk + (p.has_shared ? 1 : 0);
     hipEvent_t first = ev(0);
+    // one-row calls route inside the gate/up launch: their prepare stage is the router front
+    // alone (given gate_w), else it has no kernel and records no events
+    const bool route1 = !p.mfma && p.T == 1;
     if (p.gate_w) {
         const int waves = p.n_logits * ((p.T + GATE_ROWS - 1) / GATE_ROWS);
-        launch_timed(moe_gate_kernel, dim3((waves + 3) / 4), dim3(256), stream, first, nullptr, p,
+        launch_timed(moe_gate_kernel, dim3((waves + 3) / 4), dim3(256), stream, first, route1 ? ev(1) : nullptr, p,
                      const_cast<float*>(p.logits));
         first = nullptr;
     }
-    if (!p.mfma) {
+    if (route1) {
+        // one-row calls: the gate/up launch routes (no prepare launch, no prepare events)
+    } else if (!p.mfma) {
         // decode path: one workgroup routes, groups and writes the records; the gate/up waves
         // rotate their own inputs
         launch_timed(moe_prepare_gemv_kernel, dim3(1), dim3(256), stream, first, ev(1), p);
@@ -1782,7 +2023,12 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
             const long waves = (long)p.units_max * 2 * (p.I / 128) * ks_gate_up(p, p.units_max).base;
             const dim3 grid((unsigned)((waves + 3) / 4));
             const bool group = (p.I / 128) % ROT_WAVES == 0;
-            if (tmax == 1) {
+            if (route1) {
+                // one more workgroup publishes the routes and records
+                const dim3 grid1(grid.x + 1);
+                if (group) launch_timed(moe_gate_up_route1_kernel<true>, grid1, dim3(256), stream, ev(2), ev(3), p);
+                else launch_timed(moe_gate_up_route1_kernel<false>, grid1, dim3(256), stream, ev(2), ev(3), p);
+            } else if (tmax == 1) {
                 if (group) launch_timed(moe_gate_up_rot_kernel<1, true>, grid, dim3(256), stream, ev(2), ev(3), p);
                 else launch_timed(moe_gate_up_rot_kernel<1, false>, grid, dim3(256), stream, ev(2), ev(3), p);
             } else {

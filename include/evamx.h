@@ -149,7 +149,9 @@ typedef struct evamx_moe_args {
     /* optional: 10 hipEvent_t for the 5 stages (prepare, gate/up, activation, down,
      * combine): events[2k] takes the start timestamp of stage k's first kernel and
      * events[2k+1] the end timestamp of its last (kernel timestamps, hipExtLaunchKernel);
-     * NULL for none */
+     * NULL for none. A 1-row call routes inside its gate/up launch: its prepare stage is the
+     * router front alone when gate_w is given, and otherwise has no kernel and records no
+     * events. */
     void* const* events;
     /* optional residual stream: bf16 [rows][residual_stride], updated in place to
      * bf16(residual + bf16(out)) (the layer output cast to the activation dtype and added,
