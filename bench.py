@@ -337,6 +337,36 @@ def summarize_pmc(paths, calib_paths, copy_bytes=1 << 30, key=None):
     return "\n".join(lines)
 
 
+def summarize_counters(paths):
+    """Average per dispatch of every counter in rocprofv3 --pmc CSVs (any counters, e.g. the SQ
+    instruction and wait counters), per evamx kernel (measurement kernels included), with the
+    ratios the counters present allow: VALU instructions per wave, and the share of wave cycles
+    spent issuing VALU (SQ_ACTIVE_INST_VALU) and waiting (SQ_WAIT_INST_ANY)."""
+    import collections
+    per_kernel = collections.defaultdict(lambda: collections.defaultdict(list))
+    for p in paths:
+        for counter, per in _pmc_rows(p).items():
+            for (k, _), x in per.items():
+                if stage_of(k) or k.startswith("bench_"):
+                    per_kernel[k][counter].append(x)
+    counters = sorted({c for d in per_kernel.values() for c in d})
+    ratios = [("VALU insts / wave", "SQ_INSTS_VALU", "SQ_WAVES"),
+              ("active VALU / wave cycles", "SQ_ACTIVE_INST_VALU", "SQ_WAVE_CYCLES"),
+              ("wait / wave cycles", "SQ_WAIT_INST_ANY", "SQ_WAVE_CYCLES")]
+    ratios = [r for r in ratios if r[1] in counters and r[2] in counters]
+    lines = ["| kernel | dispatches | " + " | ".join(counters) + "".join(f" | {r[0]}" for r in ratios) + " |",
+             "|---|---|" + "---|" * (len(counters) + len(ratios))]
+    for k in sorted(per_kernel):
+        d = per_kernel[k]
+        avg = {c: sum(v) / len(v) for c, v in d.items()}
+        n = max(len(v) for v in d.values())
+        row = f"| {k} | {n} | " + " | ".join(f"{avg.get(c, 0):.4g}" for c in counters)
+        for _, num, den in ratios:
+            row += f" | {avg[num] / avg[den]:.4g}" if avg.get(den) else " | -"
+        lines.append(row + " |")
+    return "\n".join(lines)
+
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +399,8 @@ def parse_args():
     ap.add_argument("--calibration", metavar="CSV", nargs="*", default=[],
                     help="with --summarize-pmc: the counter CSVs of a --copy-calibration run")
     ap.add_argument("--traffic-key", default=None, help="with --summarize-pmc: e.g. tokens=1,bits=4")
+    ap.add_argument("--summarize-counters", metavar="CSV", nargs="+",
+                    help="print per-kernel averages of any rocprofv3 --pmc counters and exit (no GPU)")
     ap.add_argument("--skip-dispatches", type=int, default=0, help="with --summarize-trace: warm-up dispatches")
     args = ap.parse_args()
     defaults = {"layer": (1, 4.0, 4), "stack": (8, 2.5, 58), "prefill": (512, None, 2), "linear": (1, 4.0, 64)}[args.workload]
@@ -385,6 +417,9 @@ def main():
     args = parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.skip_dispatches))
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
         return
     if args.summarize_pmc:
         print(summarize_pmc(args.summarize_pmc, args.calibration, key=args.traffic_key))
@@ -745,7 +780,9 @@ def run_linear(torch, args):
                                f"{copies} resident copies in one graph (BASELINE configs[0])",
                    "in": n_in, "out": n_out, "tokens": T, "bits": bits, "copies": copies},
         "step_bytes": int(nbytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
-        "roofline": {"bound": "hbm", "kernel": "exl3_linear (3 launches per call)", "achieved": round(gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "exl3_linear (" + ("2 launches: GEMV with its input rotation, epilogue"
+                                                            if T <= 2 else "rotation, GEMV or MFMA tiles, epilogue")
+                     + " per call)", "achieved": round(gbps, 1),
                      "peak": PEAK_HBM, "unit": "GB/s", "frac": round(gbps / PEAK_HBM, 4), "traffic": None},
     }
     if not args.no_cpu_baseline:
