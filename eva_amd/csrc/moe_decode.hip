@@ -2036,14 +2036,11 @@ bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T
 
 // The table-assisted decode of one-row gate/up launches is slower on MI355X than the vector-ALU
 // decode (its LDS lookups stall every step), so it runs only when EVAMX_GATE_UP_DECODE=table is
-// set in the environment (read once), to reproduce that comparison.
+// set in the environment (read at each call), to reproduce that comparison.
 static bool table_decode_requested()
 {
-    static const bool on = [] {
-        const char* v = getenv("EVAMX_GATE_UP_DECODE");
-        return v && strcmp(v, "table") == 0;
-    }();
-    return on;
+    const char* v = getenv("EVAMX_GATE_UP_DECODE");
+    return v && strcmp(v, "table") == 0;
 }
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
