@@ -176,3 +176,35 @@ def test_one_row_table_decode_variant(dev, K):
     assert np.array_equal(outs[0], outs[1])
     ref, _, _, _ = coop.moe_layer(x, z, ex, sh, k, 10.0)
     assert rel_err_rows(outs[1], ref) < TOL
+
+
+@pytest.mark.parametrize("E,k,score,bias", [(384, 16, "sigmoid", False), (384, 8, "sqrt_softplus", True),
+                                            (64, 32, "sigmoid", True)])
+def test_one_row_routing_variants(dev, E, k, score, bias):
+    """Routing inside the gate/up launch beyond the DSv3 defaults: more than 256 experts (eight
+    keys per lane), top-16 and top-32 (the shared expert's unit after 32 routed ones), the
+    sqrt-softplus score and a selection bias (model.py:404-416). Indices and weights are the
+    oracle's bit for bit, the run table is the reference's, the output within the tolerance."""
+    from eva_amd import ops
+    H, I = 256, 128
+    rng = np.random.default_rng(46 + k)
+    ex = _experts(rng, H, I, E, 2)
+    sh = synth.expert(rng, H, I, 2, 1 / np.sqrt(H))
+    de, ds = DeviceExperts(ex, dev), DeviceExperts([sh], dev)
+    x = synth.activations_bf16(rng, 1, H)
+    z = synth.logits_plain(rng, 1, E)
+    b = (rng.standard_normal(E) * 0.5).astype(np.float32) if bias else None
+    ws = ops.MoeWorkspace(dev, rows_max=1, hidden=H, inter=I, topk=k, n_local=E, has_shared=True)
+    sel = torch.empty(1, k, dtype=torch.int64, device=dev)
+    w = torch.empty(1, k, dtype=torch.float32, device=dev)
+    out = torch.empty(1, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), de.table, out, limit=10.0, bits=2, logits=to_dev(z, dev),
+                    sel=sel, weights=w, shared_ptrs=ds.ptrs(0), shared_bits=2, score_fn=score,
+                    sel_bias=None if b is None else to_dev(b, dev), route_scale=2.5)
+    torch.cuda.synchronize()
+    ref, ridx, rw32, rrw = coop.moe_layer(x, z, ex, sh, k, 10.0, score_fn=score, sel_bias=b, route_scale=2.5)
+    assert np.array_equal(sel.cpu().numpy(), ridx)
+    assert np.array_equal(w.cpu().numpy(), rw32)
+    assert int(ws.flags().cpu()[0]) == 0
+    assert np.array_equal(ws.runs().cpu().numpy(), coop.reference_table(ridx, rrw, capacity=1))
+    assert rel_err_rows(out.cpu().numpy(), ref) < TOL
