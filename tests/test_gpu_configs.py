@@ -88,6 +88,38 @@ def test_config4_prefill_reduced(dev, limit):
             assert rel_err_rows(y, variants[name]) > 2 * TOL, name
 
 
+@pytest.mark.parametrize("T,zipf", [(512, True), (40, False)])
+def test_prefill_coop_form_matches_wave_form(dev, T, zipf):
+    """The opt-in cooperative form of the MFMA stages (EVAMX_PREFILL_FORM=coop: four waves share a
+    tile's decode through LDS) accumulates every column over the same k-steps in the same order as
+    the single-wave form, so the layer's output is bit-identical; and within the tolerance of the
+    oracle, with the SwiGLU limit clipping. 512 Zipf tokens give tiles of 1-4 row blocks; 40
+    tokens give automatic k-splits."""
+    import os
+    from eva_amd import ops
+    H, I, E, topk = 1024, 256, 64, 8
+    rng = np.random.default_rng(105 + T)
+    rates = synth.mixed_rates(rng, E)
+    experts = [synth.expert(rng, H, I, float(r), 1 / np.sqrt(H)) for r in rates]
+    shared = synth.expert(rng, H, I, 4, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, T, H)
+    logits = synth.logits_zipf(rng, T, E) if zipf else synth.logits_plain(rng, T, E)
+    de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+    outs = []
+    for form in (None, "coop"):
+        if form:
+            os.environ["EVAMX_PREFILL_FORM"] = form
+        try:
+            out, _ = _moe(ops, dev, H, I, E, topk, T, de.table, de.k2, to_dev(x, dev).to(torch.bfloat16),
+                          to_dev(logits, dev), ds.ptrs(0), 4.0, limit=CLIP)
+        finally:
+            os.environ.pop("EVAMX_PREFILL_FORM", None)
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    ref = coop.moe_layer(x, logits, experts, shared, topk, CLIP)[0]
+    assert rel_err_rows(outs[1], ref) < TOL
+
+
 class _DeviceRandomExperts:
     """E experts at per-expert rates, drawn on the device (seeded), with a [9, E] pointer table."""
 
