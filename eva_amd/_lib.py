@@ -71,6 +71,7 @@ _SIGNATURES = {
     "evamx_moe_runs_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_moe_flags_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_moe_logits_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
+    "evamx_moe_rotated_ptr": (_vp, [ctypes.POINTER(MoeShape), _vp]),
     "evamx_bench_decode": (ctypes.c_int, [_f32, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "evamx_bench_read": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
 }

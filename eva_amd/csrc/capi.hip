@@ -301,6 +301,12 @@ extern "C" float* evamx_moe_logits_ptr(const evamx_moe_shape* shape, void* works
     return (float*)((char*)workspace + moe_layout(shape).logits);
 }
 
+extern "C" const void* evamx_moe_rotated_ptr(const evamx_moe_shape* shape, void* workspace)
+{
+    if (!shape_ok(shape) || !workspace) return nullptr;
+    return (const void*)((char*)workspace + moe_layout(shape).xr);
+}
+
 extern "C" int32_t* evamx_moe_runs_ptr(const evamx_moe_shape* shape, void* workspace)
 {
     if (!shape_ok(shape) || !workspace) return nullptr;

@@ -181,6 +181,17 @@ class MoeWorkspace:
         off = addr - self.buffer.data_ptr()
         return self.buffer[off:off + 4 * rows * n_logits].view(torch.float32).view(rows, n_logits)
 
+    def rotated(self) -> torch.Tensor:
+        """fp16 ``[2, nslot_max, hidden]`` view of the rotated gate (0) and up (1) inputs the last
+        forward of 3 or more rows wrote: routed slot ``row * topk + k``, shared-expert row ``r`` at
+        ``rows * topk + r``."""
+        s = self.shape
+        nslot_max = s.rows_max * s.topk + (s.rows_max if s.has_shared else 0)
+        addr = lib().evamx_moe_rotated_ptr(ctypes.byref(s), ptr(self.buffer))
+        off = addr - self.buffer.data_ptr()
+        n = 2 * nslot_max * s.hidden
+        return self.buffer[off:off + 2 * n].view(torch.float16).view(2, nslot_max, s.hidden)
+
     def flags(self) -> torch.Tensor:
         addr = lib().evamx_moe_flags_ptr(ctypes.byref(self.shape), ptr(self.buffer))
         off = addr - self.buffer.data_ptr()

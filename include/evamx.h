@@ -198,6 +198,13 @@ int32_t* evamx_moe_flags_ptr(const evamx_moe_shape* shape, void* workspace);
  * stable_linear of model.py:404-409 / stable_linear_runtime's "router" dispatch); undefined after
  * a forward given logits. */
 float* evamx_moe_logits_ptr(const evamx_moe_shape* shape, void* workspace);
+/* The rotated gate/up inputs fp16(H128(fp16(x) * suh)) the last forward of 3 or more rows wrote,
+ * the activations the reference's rotation kernel (exl3_moe_coop_kernel.cuh:613-671) hands to its
+ * gate and up GEMVs: fp16 [2][nslot_max][hidden], projection 0 gate and 1 up, routed slot
+ * row * topk + k for each active slot, shared-expert row r at rows * topk + r, with nslot_max =
+ * rows_max * topk (+ rows_max with a shared expert). Undefined for inactive slots and after calls
+ * of 1-2 rows, whose waves rotate their inputs in LDS. */
+const void* evamx_moe_rotated_ptr(const evamx_moe_shape* shape, void* workspace);
 
 /* ---- measurement --------------------------------------------------------------------------- */
 

@@ -129,6 +129,8 @@ def test_other_entry_points_reject_bad_arguments():
     assert L.evamx_prepare_routes(FAKE, FAKE, 5, 8, 4, 256, FAKE, FAKE, 1 << 20, None) == _lib.EVAMX_EINVAL
     assert L.evamx_prepare_routes(FAKE, FAKE, 4, 8, 4, 256, FAKE, FAKE, 8, None) == _lib.EVAMX_ENOSPACE
     assert L.evamx_moe_runs_ptr(ctypes.byref(_shape(hidden=1)), FAKE) is None
+    assert L.evamx_moe_rotated_ptr(ctypes.byref(_shape(hidden=1)), FAKE) is None
+    assert L.evamx_moe_rotated_ptr(ctypes.byref(_shape()), None) is None
     assert L.evamx_bench_decode(4.25, 4096, 10, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_bench_decode(4.0, 4094, 10, FAKE, None) == _lib.EVAMX_EINVAL
     assert L.evamx_bench_decode(4.0, 4096, 0, FAKE, None) == _lib.EVAMX_EINVAL

@@ -419,6 +419,46 @@ def test_moe_bf16_x_rounds_to_fp16(dev, rows):
         assert rel_err_rows(y[1:], ref[1:]) < TOL
 
 
+@pytest.mark.parametrize("rows", [4, 40])
+def test_rotated_inputs_bit_exact(dev, rows):
+    """The input rotation on its own (K.cuh:613-629): every active routed slot's and every
+    shared row's gate and up inputs fp16(H128(fp16(x) * suh)) in the workspace equal the oracle's
+    bit for bit (same fp32 butterfly order, same roundings), with bf16 activations that include
+    fp16-subnormal-range values. 4 rows rotate in the small prepare, 40 in the rotation kernel of
+    the prefill path; zero routing weights leave some slots inactive."""
+    ops = _ops()
+    H, I, E, topk, K = 512, 256, 16, 4, 4
+    rng = np.random.default_rng(700 + rows)
+    experts, shared = _layer_case(rng, H, I, E, K, 1 / np.sqrt(H))
+    x = synth.activations_bf16(rng, rows, H)
+    x[:, 3] = np.array([3.0e-5, -1.1e-6, 6.0e-7, -4.4e-5] * rows, np.float32)[:rows]
+    x = coop.round_bf16(x)
+    sel = rng.integers(0, E, size=(rows, topk)).astype(np.int64)
+    rw = rng.uniform(0.1, 1.0, size=(rows, topk)).astype(np.float16)
+    rw[rng.random((rows, topk)) < 0.2] = 0
+    de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=True)
+    out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), de.table, out, limit=10.0, bits=K,
+                    sel=to_dev(sel, dev), rw=to_dev(rw, dev), shared_ptrs=ds.ptrs(0), shared_bits=K)
+    torch.cuda.synchronize()
+    assert int(ws.flags().cpu()[0]) == 0
+    xr = ws.rotated().cpu().numpy()
+    x16 = x.astype(np.float16)
+    checked = 0
+    for pi, p in enumerate(("g", "u")):
+        for r in range(rows):
+            for k in range(topk):
+                if rw[r, k] == 0:
+                    continue
+                ref = coop.rotate_input(x16[r], experts[sel[r, k]].suh(p))
+                assert np.array_equal(xr[pi, r * topk + k].view(np.uint16), ref.view(np.uint16)), (p, r, k)
+                checked += 1
+            ref = coop.rotate_input(x16[r], shared.suh(p))
+            assert np.array_equal(xr[pi, rows * topk + r].view(np.uint16), ref.view(np.uint16)), (p, "shared", r)
+    assert checked > rows * topk
+
+
 def test_moe_out_of_range_expert_sets_flag(dev):
     ops = _ops()
     H, I, E, topk = 256, 128, 8, 2
