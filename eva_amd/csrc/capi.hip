@@ -333,7 +333,7 @@ extern "C" int evamx_moe_forward(const evamx_moe_args* a, evamx_stream_t stream)
 {
     g_err[0] = 0;
     EVAMX_REQUIRE(a, "evamx_moe_forward: null args");
-    return moe_forward_ws(a, a->workspace, a->workspace_bytes, (hipStream_t)stream, "evamx_moe_forward");
+    return moe_forward_ws(a, a->workspace, a->workspace_bytes, (hipStream_t)stream, "evamx_moe_forward", true);
 }
 
 size_t evamx::moe_workspace_bytes_of(const evamx_moe_shape* shape)
@@ -349,7 +349,7 @@ int evamx::moe_flags_offset(const evamx_moe_shape* shape, size_t* off)
 }
 
 int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                          const char* who)
+                          const char* who, bool side_stream_ok)
 {
     const evamx_moe_shape* s = &a->shape;
     if (!shape_ok(s)) return EVAMX_EINVAL;
@@ -456,6 +456,7 @@ int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t works
     p.ks_gu_max = L.ks_gu_max; p.ks_d_max = L.ks_d_max;
     p.cap_rows_gu = L.cap_rows_gu; p.cap_rows_d = L.cap_rows_d;
     p.gemv_waves = gemv_waves();
+    p.side_ok = side_stream_ok ? 1 : 0;
     p.out = a->out; p.out_stride = a->out_stride;
     p.residual = (uint16_t*)a->residual; p.residual_stride = a->residual_stride;
     moe_launch(p, stream, a->events);

@@ -11,9 +11,10 @@ void set_error(const char* fmt, ...);
 
 // The MoE forward of evamx_moe_forward on a given workspace (validation included); `who` names
 // the entry point in error messages. Used by the entry points with a caller's workspace and with
-// the library's fixed device scratch.
+// the library's fixed device scratch; side_stream_ok lets calls of more than 16 tokens run their
+// MFMA stages' two kernels concurrently on a side stream (the fixed-scratch entry point creates none).
 int moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                   const char* who);
+                   const char* who, bool side_stream_ok);
 size_t moe_workspace_bytes_of(const evamx_moe_shape* shape);
 int moe_flags_offset(const evamx_moe_shape* shape, size_t* off);
 // n ints at p set to v by a kernel on `stream` (capture-safe, unlike a memset node)

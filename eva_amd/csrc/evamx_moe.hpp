@@ -115,6 +115,9 @@ struct MoeParams {
     int ks_gu_max, ks_d_max;   // bounds of the automatic choice
     int cap_rows_gu, cap_rows_d;   // partial-buffer capacity in rows (ks * nslot <= cap)
     int gemv_waves;            // grid of the GEMV kernels (waves resident on the device at once)
+    int force_split;           // MFMA stages: tiles of at most 16 rows always in the 16-row kernel
+    int side_ok;               // host: the MFMA stages may use the thread's side stream (not for the
+                               // allocation-free entry point)
     UnitRec* urec;             // decode path: [units_max] work-unit records
     SlotRec* srec;             // decode path: [T * topk + T] slot records (routed slots, shared rows)
     int units_max;             // decode path: work units the launch grids cover (T * topk + has_shared)

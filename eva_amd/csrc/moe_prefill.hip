@@ -84,7 +84,7 @@ __device__ __forceinline__ void mfma_stage(const MoeParams& p, uint32_t (&lds)[M
     // this launch's tiles: the small ones (at most 16 rows) in the MBMAX 1 kernel when they fill
     // at least three of its resident rounds (3 waves per SIMD), so that its last round's tail is
     // short; the rest (or all) in the MBMAX 4 kernel. Up to 16 tokens every tile is small.
-    const bool split = p.T <= EVAMX_SMALL_TILE_ROWS || (long)n_small * per_tile >= 3L * (p.gemv_waves * 3 / 4);
+    const bool split = p.force_split || p.T <= EVAMX_SMALL_TILE_ROWS || (long)n_small * per_tile >= 3L * (p.gemv_waves * 3 / 4);
     const int n_tiles = MBMAX == 1 ? (split ? n_small : 0) : (split ? n_all - n_small : n_all);
     // the call's items fill the first n_blk workgroups (a multiple of 8, spread over the XCDs)
     const int n_blk = ((n_tiles * per_tile + MF_WAVES - 1) / MF_WAVES + 7) & ~7;
@@ -274,6 +274,53 @@ static bool coop_form_requested()
     return v && strcmp(v, "coop") == 0;
 }
 
+// Side stream of the calling thread on the current device, with its fork and join events, for
+// the concurrent MFMA launches of calls of more than 16 tokens. One per thread and device (a
+// thread's calls and captures are ordered, so its side stream never joins another thread's
+// capture); created on the thread's first such call outside stream capture and kept until the
+// process ends, at default priority. nullptr, and the launches stay on the caller's stream, when
+// it does not exist and cannot be made (the caller's stream is capturing, a creation failed, an
+// earlier error is pending) or when EVAMX_PREFILL_CONCURRENT=0 is set in the environment (read at
+// each call, to reproduce the comparison).
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int SIDE_MAX_DEVICES = 64;
+
+static const SideStream* side_stream(hipStream_t stream)
+{
+    static thread_local SideStream side[SIDE_MAX_DEVICES];
+    const char* v = getenv("EVAMX_PREFILL_CONCURRENT");
+    if (v && strcmp(v, "0") == 0) return nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SIDE_MAX_DEVICES) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    SideStream& ss = side[dev];
+    if (ss.s) return &ss;
+    if (hipPeekAtLastError() != hipSuccess) return nullptr;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    SideStream made;
+    if (hipStreamCreateWithFlags(&made.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&made.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&made.join, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        if (made.join) (void)hipEventDestroy(made.join);
+        if (made.fork) (void)hipEventDestroy(made.fork);
+        if (made.s) (void)hipStreamDestroy(made.s);
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    ss = made;
+    return &ss;
+}
+
 // Launch of one projection stage: enough workgroups for the largest possible item count (the
 // workspace's tile bound times the largest split); workgroups past the call's items exit at once.
 int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
@@ -304,6 +351,19 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
         // cooperative form: one item per workgroup
         const dim3 wg_grid((unsigned)((items + 7) & ~7L));
         launch_timed(which == 0 ? moe_gate_up_wg_kernel : moe_down_wg_kernel, wg_grid, block, stream, start, stop, p);
+    } else if (const SideStream* side = p.T > EVAMX_SMALL_TILE_ROWS && p.side_ok ? side_stream(stream) : nullptr) {
+        // the tiles of at most 16 rows in the 16-row kernel on the side stream, concurrently with
+        // the larger ones in the 64-row kernel on the caller's stream: each fills the other's
+        // last round (two kernels of different register budgets cannot share one grid)
+        MoeParams q = p;
+        q.force_split = 1;
+        hipEventRecord(side->fork, stream);
+        hipStreamWaitEvent(side->s, side->fork, 0);
+        launch_timed(k64, grid, block, stream, start, nullptr, q);
+        launch_timed(k16, grid, block, side->s, nullptr, nullptr, q);
+        hipEventRecord(side->join, side->s);
+        hipStreamWaitEvent(stream, side->join, 0);
+        if (stop) hipEventRecord(stop, stream);
     } else if (p.T <= EVAMX_SMALL_TILE_ROWS) {
         launch_timed(k16, grid, block, stream, start, stop, p);
     } else if (!may_split) {

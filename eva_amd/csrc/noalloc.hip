@@ -79,5 +79,5 @@ extern "C" int evamx_moe_forward_static(const evamx_moe_args* a, evamx_stream_t 
     void* ws = nullptr;
     const int rc = device_scratch(&ws, (hipStream_t)stream);
     if (rc != EVAMX_OK) return rc;
-    return moe_forward_ws(a, ws, STATIC_SCRATCH_BYTES, (hipStream_t)stream, "evamx_moe_forward_static");
+    return moe_forward_ws(a, ws, STATIC_SCRATCH_BYTES, (hipStream_t)stream, "evamx_moe_forward_static", false);
 }

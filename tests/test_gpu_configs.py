@@ -89,12 +89,14 @@ def test_config4_prefill_reduced(dev, limit):
 
 
 @pytest.mark.parametrize("T,zipf", [(512, True), (40, False)])
-def test_prefill_coop_form_matches_wave_form(dev, T, zipf):
-    """The opt-in cooperative form of the MFMA stages (EVAMX_PREFILL_FORM=coop: four waves share a
-    tile's decode through LDS) accumulates every column over the same k-steps in the same order as
-    the single-wave form, so the layer's output is bit-identical; and within the tolerance of the
-    oracle, with the SwiGLU limit clipping. 512 Zipf tokens give tiles of 1-4 row blocks; 40
-    tokens give automatic k-splits."""
+def test_prefill_forms_bit_identical(dev, T, zipf):
+    """The MFMA stages' launch forms accumulate every column over the same k-steps in the same
+    order, so the layer's output is bit-identical across them: the default (tiles of at most 16
+    rows in the 16-row kernel on a side stream, concurrently with the larger ones),
+    EVAMX_PREFILL_CONCURRENT=0 (one kernel on the caller's stream), and the opt-in cooperative
+    form (EVAMX_PREFILL_FORM=coop: four waves share a tile's decode through LDS); and within the
+    tolerance of the oracle, with the SwiGLU limit clipping. 512 Zipf tokens give tiles of 1-4
+    row blocks; 40 tokens give automatic k-splits."""
     import os
     from eva_amd import ops
     H, I, E, topk = 1024, 256, 64, 8
@@ -106,16 +108,17 @@ def test_prefill_coop_form_matches_wave_form(dev, T, zipf):
     logits = synth.logits_zipf(rng, T, E) if zipf else synth.logits_plain(rng, T, E)
     de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
     outs = []
-    for form in (None, "coop"):
-        if form:
-            os.environ["EVAMX_PREFILL_FORM"] = form
+    for env in ({}, {"EVAMX_PREFILL_CONCURRENT": "0"}, {"EVAMX_PREFILL_FORM": "coop"}):
+        os.environ.update(env)
         try:
             out, _ = _moe(ops, dev, H, I, E, topk, T, de.table, de.k2, to_dev(x, dev).to(torch.bfloat16),
                           to_dev(logits, dev), ds.ptrs(0), 4.0, limit=CLIP)
         finally:
-            os.environ.pop("EVAMX_PREFILL_FORM", None)
+            for key in env:
+                os.environ.pop(key, None)
         outs.append(out.cpu().numpy())
     assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[2])
     ref = coop.moe_layer(x, logits, experts, shared, topk, CLIP)[0]
     assert rel_err_rows(outs[1], ref) < TOL
 

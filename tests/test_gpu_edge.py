@@ -111,11 +111,14 @@ def test_workspace_reuse_smaller_call(dev):
         assert np.array_equal(ws.runs().cpu().numpy(), coop.reference_table(sel, rw, capacity=16))   # no stale entries
 
 
-def test_graph_replays(dev):
+@pytest.mark.parametrize("T", [2, 40])
+def test_graph_replays(dev, T):
     """Captured forward (routing included), replayed with new inputs copied into the static
-    buffers between replays; every replay equals the eager result for the same inputs."""
+    buffers between replays; every replay equals the eager result for the same inputs. At 40
+    tokens the MFMA stages run their two kernels concurrently (the side stream joins the
+    capture)."""
     from eva_amd import ops
-    H, I, E, k, T = 256, 128, 16, 4, 2
+    H, I, E, k = 256, 128, 16, 4
     rng = np.random.default_rng(35)
     ex = _experts(rng, H, I, E, 4)
     sh = synth.expert(rng, H, I, 4, 1 / np.sqrt(H))
