@@ -251,29 +251,43 @@ def stage_of(short):
 
 def summarize_trace(path, skip=0):
     """Per-kernel dispatch count and durations (µs) of a rocprofv3 --kernel-trace CSV, evamx
-    kernels only, after dropping each kernel's first ``skip`` dispatches (warm-up), and the sum
-    per forward of each MoE stage (forwards = dispatches of the combine stage)."""
+    kernels only, after dropping each kernel's first ``skip`` dispatches (warm-up), and the time
+    per forward of each MoE stage (forwards = dispatches of the combine stage). A stage's time is
+    the wall-clock span of each of its occurrences (consecutive dispatches of the stage in start
+    order, from the first start to the last end), so two kernels of one stage that run
+    concurrently count once."""
     import csv
     import collections
     durs = collections.defaultdict(list)
+    events = []
     for row in csv.DictReader(open(path)):
         short = kernel_short_name(row["Kernel_Name"])
         if not row["Kernel_Name"].strip().startswith(("void evamx::", "evamx::", "_ZN5evamx")):
             continue
-        durs[short].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+        t0, t1 = int(row["Start_Timestamp"]), int(row["End_Timestamp"])
+        durs[short].append((t1 - t0) / 1e3)
+        events.append((t0, t1, stage_of(short)))
     lines = ["| kernel | dispatches | avg µs | median µs | min µs | max µs |", "|---|---|---|---|---|---|"]
-    stage_tot = collections.defaultdict(float)
     n_fwd = 0
     for k in sorted(durs):
         d = durs[k][skip:] or durs[k]
         lines.append(f"| {k} | {len(d)} | {sum(d) / len(d):.2f} | {median(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
-        st = stage_of(k)
-        if st:
-            stage_tot[st] += sum(d)
-        if st == "combine":
+        if stage_of(k) == "combine":
             n_fwd += len(d)
+    stage_tot = collections.defaultdict(float)
+    events.sort()
+    i = 0
+    while i < len(events):
+        t0, t1, st = events[i]
+        j = i + 1
+        while j < len(events) and events[j][2] == st:
+            t1 = max(t1, events[j][1])
+            j += 1
+        if st:
+            stage_tot[st] += (t1 - t0) / 1e3
+        i = j
     if n_fwd:
-        lines += ["", f"per forward ({n_fwd} forwards): " + ", ".join(
+        lines += ["", f"per forward ({n_fwd} forwards; stage spans, concurrent kernels counted once): " + ", ".join(
             f"{st} {stage_tot[st] / n_fwd:.2f} µs" for st, _ in STAGES if st in stage_tot)]
     return "\n".join(lines)
 
