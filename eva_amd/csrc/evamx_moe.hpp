@@ -116,6 +116,8 @@ struct MoeParams {
     int cap_rows_gu, cap_rows_d;   // partial-buffer capacity in rows (ks * nslot <= cap)
     int gemv_waves;            // grid of the GEMV kernels (waves resident on the device at once)
     int force_split;           // MFMA stages: tiles of at most 16 rows always in the 16-row kernel
+    int act_class;             // activation stage: 0 every row; 1 the rows of tiles of at most 16 rows;
+                               // 2 the rows of larger tiles (a size class pipelined on its own stream)
     int side_ok;               // host: the MFMA stages may use the thread's side stream (not for the
                                // allocation-free entry point)
     UnitRec* urec;             // decode path: [units_max] work-unit records
@@ -222,6 +224,18 @@ inline void launch_timed(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStr
 }
 
 int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// One size class of an MFMA stage on its own: cls 1 the tiles of at most 16 rows (16-row kernel),
+// cls 2 the larger ones (64-row kernel); both read the split tile list.
+int launch_mfma_class(const MoeParams& p, int which, int cls, hipStream_t stream);
+// The calling thread's side stream on the current device with its fork and join events, or
+// nullptr (see moe_prefill.hip).
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+const SideStream* side_stream(hipStream_t stream);
+// EVAMX_PREFILL_FORM=coop: the opt-in cooperative form of the MFMA stages (moe_prefill.hip).
+bool prefill_coop_form_requested();
 int moe_prepare_only(MoeParams& p, hipStream_t stream);
 int launch_router_logits(const MoeParams& p, float* logits, hipStream_t stream);
 bool moe_small_path(int T, int topk);

@@ -1687,9 +1687,28 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int na = p.I / 128;
     const int ng = na / CPW;                 // chunk groups per row (CPW divides na)
-    const int n_rows = REC ? moe_nslot(p) : p.meta[1] + (p.has_shared ? p.T : 0);
-    if (wid >= n_rows * ng) return;
-    const int o = wid / ng, a0 = (wid % ng) * CPW;
+    int o, a0;
+    if (!REC && p.act_class) {
+        // one size class of the MFMA tiles: wave -> (tile of the class, row of the tile up to the
+        // class's row bound, chunk group); rows past the tile's exit at once
+        const int cap = p.act_class == 1 ? EVAMX_SMALL_TILE_ROWS : EVAMX_TILE_ROWS;
+        const int n_small = __builtin_amdgcn_readfirstlane(p.meta[3]);
+        const int n_cls = p.act_class == 1 ? n_small : __builtin_amdgcn_readfirstlane(p.meta[0]) - n_small;
+        const int ti = wid / (cap * ng);
+        if (ti >= n_cls) return;
+        const int rem = wid - ti * cap * ng;
+        const int r = rem / ng;
+        a0 = (rem % ng) * CPW;
+        const int tile = __builtin_amdgcn_readfirstlane(p.act_class == 1 ? p.tiles[ti] : p.tiles[p.max_chunks - 1 - ti]);
+        const int* ch = p.chunks + 8 * tile;
+        if (r >= __builtin_amdgcn_readfirstlane(ch[2])) return;
+        o = __builtin_amdgcn_readfirstlane(ch[1]) + r;
+    } else {
+        const int n_rows = REC ? moe_nslot(p) : p.meta[1] + (p.has_shared ? p.T : 0);
+        if (wid >= n_rows * ng) return;
+        o = wid / ng;
+        a0 = (wid % ng) * CPW;
+    }
     int s, Sg;
     bool shared;
     const half_t *g_svh, *u_svh, *d_suh;
@@ -1804,6 +1823,23 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
 
 // Activation launch: one wave per (row, chunk) for small batches (latency), per (row, 4 chunks)
 // for large ones (the row's slot, expert and pointers resolved once).
+// The activation stage for the rows of one size class of MFMA tiles (cls 1: tiles of at most 16
+// rows, cls 2: larger), calls of more than 16 tokens.
+static void launch_act_class(const MoeParams& p, int cls, hipStream_t stream)
+{
+    const int na = p.I / 128;
+    MoeParams q = p;
+    q.act_class = cls;
+    const long cap = cls == 1 ? EVAMX_SMALL_TILE_ROWS : EVAMX_TILE_ROWS;
+    if (p.T > EVAMX_SMALL_ROWS && na % 4 == 0) {
+        const long waves = (long)p.max_chunks * cap * (na / 4);
+        launch_timed(moe_act_kernel<4, false>, dim3((unsigned)((waves + 3) / 4)), dim3(256), stream, nullptr, nullptr, q);
+    } else {
+        const long waves = (long)p.max_chunks * cap * na;
+        launch_timed(moe_act_kernel<1, false>, dim3((unsigned)((waves + 3) / 4)), dim3(256), stream, nullptr, nullptr, q);
+    }
+}
+
 static void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
 {
     const int na = p.I / 128;
@@ -2089,7 +2125,26 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         launch_timed(moe_group_kernel, dim3(1), dim3(64 * GROUP_WAVES), stream, first, nullptr, p);
         launch_timed(moe_rotate_kernel, dim3(EVAMX_ROTATE_BLOCKS), dim3(256), stream, nullptr, ev(1), p);
     }
-    if (p.mfma) {
+    const SideStream* side = p.mfma && p.T > EVAMX_SMALL_TILE_ROWS && p.side_ok && !events && !prefill_coop_form_requested()
+                                 ? side_stream(stream) : nullptr;
+    if (side) {
+        // calls of more than 16 tokens: each size class of tiles runs gate/up, activation and
+        // down on a stream of its own (the larger tiles' 64-row kernels on the caller's stream,
+        // the small tiles' 16-row kernels on the side stream), joined before the combine, so
+        // one class's stages fill the other's last rounds and the activation launches' idle
+        // GPU. With events the stages run one after the other (each stage's two kernels at once),
+        // so that each stage's times can be read.
+        (void)hipEventRecord(side->fork, stream);
+        (void)hipStreamWaitEvent(side->s, side->fork, 0);
+        launch_mfma_class(p, 0, 2, stream);
+        launch_act_class(p, 2, stream);
+        launch_mfma_class(p, 1, 2, stream);
+        launch_mfma_class(p, 0, 1, side->s);
+        launch_act_class(p, 1, side->s);
+        launch_mfma_class(p, 1, 1, side->s);
+        (void)hipEventRecord(side->join, side->s);
+        (void)hipStreamWaitEvent(stream, side->join, 0);
+    } else if (p.mfma) {
         launch_mfma(p, 0, stream, ev(2), ev(3));
         launch_act(p, nslot, stream, ev(4), ev(5));
         launch_mfma(p, 1, stream, ev(6), ev(7));

@@ -268,7 +268,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(M
 // EVAMX_PREFILL_FORM=coop is set in the environment (read at each call): on MI355X it is no faster
 // than the single-wave form at 512 tokens (gate/up level, down 20% slower), and it is kept to
 // reproduce that comparison. Both forms give bit-identical partials.
-static bool coop_form_requested()
+bool prefill_coop_form_requested()
 {
     const char* v = getenv("EVAMX_PREFILL_FORM");
     return v && strcmp(v, "coop") == 0;
@@ -282,13 +282,9 @@ static bool coop_form_requested()
 // it does not exist and cannot be made (the caller's stream is capturing, a creation failed, an
 // earlier error is pending) or when EVAMX_PREFILL_CONCURRENT=0 is set in the environment (read at
 // each call, to reproduce the comparison).
-struct SideStream {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-};
 constexpr int SIDE_MAX_DEVICES = 64;
 
-static const SideStream* side_stream(hipStream_t stream)
+const SideStream* side_stream(hipStream_t stream)
 {
     static thread_local SideStream side[SIDE_MAX_DEVICES];
     const char* v = getenv("EVAMX_PREFILL_CONCURRENT");
@@ -321,6 +317,38 @@ static const SideStream* side_stream(hipStream_t stream)
     return &ss;
 }
 
+// The largest possible item count of one projection stage: the workspace's tile bound times the
+// largest split (an automatic split fills one resident round; gate/up: up to two, see ks_gate_up).
+static long mfma_items(const MoeParams& p, int which)
+{
+    const int ncg = which == 0 ? p.I / 128 : p.H / 128;
+    const int kreq = which == 0 ? p.ks_gu : p.ks_d;
+    const long per_tile = (long)(which == 0 ? 2 * ncg : ncg);
+    const long auto_items = (long)(which == 0 ? 2 : 1) * p.gemv_waves + per_tile;
+    return kreq > 0 ? (long)p.max_chunks * per_tile * kreq
+                    : (p.max_chunks * per_tile > auto_items ? (long)p.max_chunks * per_tile : auto_items);
+}
+
+// Grid of one projection stage in the single-wave form: enough workgroups for mfma_items (a
+// multiple of 8); workgroups past the call's items exit at once.
+static dim3 mfma_grid(const MoeParams& p, int which)
+{
+    const long blocks = (mfma_items(p, which) + MF_WAVES - 1) / MF_WAVES;
+    return dim3((unsigned)((blocks + 7) & ~7L));
+}
+
+int launch_mfma_class(const MoeParams& p, int which, int cls, hipStream_t stream)
+{
+    MoeParams q = p;
+    q.force_split = 1;
+    const dim3 grid = mfma_grid(p, which), block(64 * MF_WAVES);
+    if (cls == 1)
+        launch_timed(which == 0 ? moe_gate_up_mfma_kernel<1> : moe_down_mfma_kernel<1>, grid, block, stream, nullptr, nullptr, q);
+    else
+        launch_timed(which == 0 ? moe_gate_up_mfma_kernel<4> : moe_down_mfma_kernel<4>, grid, block, stream, nullptr, nullptr, q);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // Launch of one projection stage: enough workgroups for the largest possible item count (the
 // workspace's tile bound times the largest split); workgroups past the call's items exit at once.
 int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
@@ -329,12 +357,7 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     const int kreq = which == 0 ? p.ks_gu : p.ks_d;
     const int kmax = which == 0 ? p.ks_gu_max : p.ks_d_max;
     const long per_tile = (long)(which == 0 ? 2 * ncg : ncg);
-    // an automatic split fills one resident round (gate/up: up to two, see ks_gate_up)
-    const long auto_items = (long)(which == 0 ? 2 : 1) * p.gemv_waves + per_tile;
-    const long items = kreq > 0 ? (long)p.max_chunks * per_tile * kreq
-                                : (p.max_chunks * per_tile > auto_items ? (long)p.max_chunks * per_tile : auto_items);
-    long blocks = (items + MF_WAVES - 1) / MF_WAVES;
-    blocks = (blocks + 7) & ~7L;
+    const long items = mfma_items(p, which);
     // tiles of at most 16 rows run in the 16-row kernel (3 waves per SIMD, progress priorities),
     // larger ones in the 64-row kernel; up to 16 tokens every tile is a small one
     // The small-tile launch is skipped when the split can never happen: at most one tile per
@@ -346,8 +369,8 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     const bool may_split = max_small * per_tile * s_max >= 3L * (p.gemv_waves * 3 / 4);
     auto k16 = which == 0 ? moe_gate_up_mfma_kernel<1> : moe_down_mfma_kernel<1>;
     auto k64 = which == 0 ? moe_gate_up_mfma_kernel<4> : moe_down_mfma_kernel<4>;
-    const dim3 grid((unsigned)blocks), block(64 * MF_WAVES);
-    if (p.T > EVAMX_SMALL_TILE_ROWS && coop_form_requested()) {
+    const dim3 grid = mfma_grid(p, which), block(64 * MF_WAVES);
+    if (p.T > EVAMX_SMALL_TILE_ROWS && prefill_coop_form_requested()) {
         // cooperative form: one item per workgroup
         const dim3 wg_grid((unsigned)((items + 7) & ~7L));
         launch_timed(which == 0 ? moe_gate_up_wg_kernel : moe_down_wg_kernel, wg_grid, block, stream, start, stop, p);
@@ -357,13 +380,13 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
         // last round (two kernels of different register budgets cannot share one grid)
         MoeParams q = p;
         q.force_split = 1;
-        hipEventRecord(side->fork, stream);
-        hipStreamWaitEvent(side->s, side->fork, 0);
+        (void)hipEventRecord(side->fork, stream);
+        (void)hipStreamWaitEvent(side->s, side->fork, 0);
         launch_timed(k64, grid, block, stream, start, nullptr, q);
         launch_timed(k16, grid, block, side->s, nullptr, nullptr, q);
-        hipEventRecord(side->join, side->s);
-        hipStreamWaitEvent(stream, side->join, 0);
-        if (stop) hipEventRecord(stop, stream);
+        (void)hipEventRecord(side->join, side->s);
+        (void)hipStreamWaitEvent(stream, side->join, 0);
+        if (stop) (void)hipEventRecord(stop, stream);
     } else if (p.T <= EVAMX_SMALL_TILE_ROWS) {
         launch_timed(k16, grid, block, stream, start, stop, p);
     } else if (!may_split) {
