@@ -286,9 +286,23 @@ def summarize_trace(path, skip=0):
         if st:
             stage_tot[st] += (t1 - t0) / 1e3
         i = j
+    # forward wall time: from a forward's first MoE kernel start to the end of its combine
+    fwd_spans, first = [], None
+    for t0, t1, st in events:
+        if not st:
+            continue
+        if first is None:
+            first = t0
+        if st == "combine":
+            fwd_spans.append((t1 - first) / 1e3)
+            first = None
     if n_fwd:
         lines += ["", f"per forward ({n_fwd} forwards; stage spans, concurrent kernels counted once): " + ", ".join(
             f"{st} {stage_tot[st] / n_fwd:.2f} µs" for st, _ in STAGES if st in stage_tot)]
+    if fwd_spans:
+        lines.append(f"forward wall time (first MoE kernel start to combine end): median {median(fwd_spans):.2f} µs "
+                     f"over {len(fwd_spans)} forwards (stages that overlap across streams make the stage spans "
+                     f"add up to more)")
     return "\n".join(lines)
 
 
