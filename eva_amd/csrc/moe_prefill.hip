@@ -280,8 +280,9 @@ bool prefill_coop_form_requested()
 // capture); created on the thread's first such call outside stream capture and kept until the
 // process ends, at default priority. nullptr, and the launches stay on the caller's stream, when
 // it does not exist and cannot be made (the caller's stream is capturing, a creation failed, an
-// earlier error is pending) or when EVAMX_PREFILL_CONCURRENT=0 is set in the environment (read at
-// each call, to reproduce the comparison).
+// earlier error is pending), when it is still joined into a capture other than the caller's, or
+// when EVAMX_PREFILL_CONCURRENT=0 is set in the environment (read at each call, to reproduce the
+// comparison).
 constexpr int SIDE_MAX_DEVICES = 64;
 
 const SideStream* side_stream(hipStream_t stream)
@@ -294,14 +295,29 @@ const SideStream* side_stream(hipStream_t stream)
         (void)hipGetLastError();
         return nullptr;
     }
-    SideStream& ss = side[dev];
-    if (ss.s) return &ss;
     if (hipPeekAtLastError() != hipSuccess) return nullptr;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    unsigned long long cap_id = 0;
+    if (hipStreamGetCaptureInfo(stream, &cap, &cap_id) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;
     }
+    SideStream& ss = side[dev];
+    if (ss.s) {
+        // a side stream joined into a capture stays in it until the capture ends: fork only
+        // from that capture's streams, or, outside any capture, only when it is free
+        hipStreamCaptureStatus side_cap = hipStreamCaptureStatusNone;
+        unsigned long long side_id = 0;
+        if (hipStreamGetCaptureInfo(ss.s, &side_cap, &side_id) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        if (side_cap == hipStreamCaptureStatusActive && (cap != hipStreamCaptureStatusActive || side_id != cap_id))
+            return nullptr;
+        if (side_cap != hipStreamCaptureStatusNone && side_cap != hipStreamCaptureStatusActive) return nullptr;
+        return &ss;
+    }
+    if (cap != hipStreamCaptureStatusNone) return nullptr;
     SideStream made;
     if (hipStreamCreateWithFlags(&made.s, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&made.fork, hipEventDisableTiming) != hipSuccess ||

@@ -111,6 +111,46 @@ def test_workspace_reuse_smaller_call(dev):
         assert np.array_equal(ws.runs().cpu().numpy(), coop.reference_table(sel, rw, capacity=16))   # no stale entries
 
 
+def test_eager_call_during_another_capture(dev):
+    """A 40-token forward captured on one stream joins the thread's side stream into that
+    capture; an eager 40-token call the same thread makes on another stream before the capture
+    ends must not fork onto it (it runs on its own stream), and both the eager result and the
+    graph's replay equal a plain eager call."""
+    from eva_amd import ops
+    H, I, E, k, T = 256, 128, 16, 4, 40
+    rng = np.random.default_rng(36)
+    ex = _experts(rng, H, I, E, 4)
+    sh = synth.expert(rng, H, I, 4, 1 / np.sqrt(H))
+    de, ds = DeviceExperts(ex, dev), DeviceExperts([sh], dev)
+    x = to_dev(synth.activations_bf16(rng, T, H), dev).to(torch.bfloat16)
+    z = to_dev(synth.logits_plain(rng, T, E), dev)
+
+    def make():
+        ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=k, n_local=E, has_shared=True)
+        sel = torch.empty(T, k, dtype=torch.int64, device=dev)
+        w = torch.empty(T, k, dtype=torch.float32, device=dev)
+        out = torch.empty(T, H, dtype=torch.float32, device=dev)
+        return lambda: ops.moe_forward(ws, x, de.table, out, limit=10.0, bits=4, logits=z, sel=sel, weights=w,
+                                       shared_ptrs=ds.ptrs(0), shared_bits=4), out
+
+    f_ref, out_ref = make()
+    f_ref()                                             # eager: creates the side stream
+    torch.cuda.synchronize()
+    f_cap, out_cap = make()
+    f_eager, out_eager = make()
+    other = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        f_cap()
+        with torch.cuda.stream(other):
+            f_eager()                                   # eager, while the side stream is in the capture
+    torch.cuda.synchronize()
+    assert torch.equal(out_eager, out_ref)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out_cap, out_ref)
+
+
 @pytest.mark.parametrize("T", [2, 40])
 def test_graph_replays(dev, T):
     """Captured forward (routing included), replayed with new inputs copied into the static
