@@ -351,12 +351,16 @@ def test_moe_given_routes_repeating_an_expert(dev, rows):
     assert rel_err_rows(out.cpu().numpy(), ref) < TOL
 
 
-@pytest.mark.parametrize("rows,pattern", [(3, "all_one"), (16, "hot_twice"), (2, "all_one"), (20, "hot_twice")])
+@pytest.mark.parametrize("rows,pattern", [(3, "all_one"), (16, "hot_twice"), (2, "all_one"), (20, "hot_twice"),
+                                          (17, "all_one"), (72, "hot_twice")])
 def test_moe_repeated_expert_fills_many_tiles(dev, rows, pattern):
     """Given routes repeating an expert inside tokens put more slots on one expert than a 16-row
     MFMA tile holds: T=3 with all 24 slots on one expert, T=16 with one expert twice in every
     token (32 slots), against the oracle over a workspace filled with garbage first (a tile
-    whose partials were never written would read it)."""
+    whose partials were never written would read it). Past 16 tokens one expert spans tiles of
+    both size classes, which run gate/up, activation and down on different streams: T=17 puts
+    136 slots on one expert (tiles of 64, 64 and 8 rows), T=72 144 slots on one (64, 64, 16)
+    and the shared expert 72 rows (64 and 8)."""
     ops = _ops()
     H, I, E, topk, limit = 256, 256, 6, 8, CLIP
     rng = np.random.default_rng(400 + rows)
