@@ -19,6 +19,12 @@
 // The LDS exchange stays within a wave (a wave's LDS instructions execute in order), so the
 // waves of a workgroup never synchronise.
 //
+// Calls of more than 16 tokens run two kernels per stage: the tiles of at most 16 rows in the
+// 16-row kernel (a quarter of the accumulators, 4 waves per SIMD) on the calling thread's side
+// stream, the larger ones in the 64-row kernel (2 waves per SIMD) on the caller's stream, at the
+// same time; moe_launch pipelines each size class through gate/up, activation and down on its
+// stream (launch_mfma_class), launch_mfma runs one stage's two kernels at once.
+//
 // An opt-in cooperative form (moe_gate_up_wg_kernel / moe_down_wg_kernel, EVAMX_PREFILL_FORM=coop)
 // gives one item to a whole workgroup: its four waves decode a quarter of each stage's k-slices
 // each, stage the A rows once through LDS, and each run the MFMAs of 32 of the 128 columns
