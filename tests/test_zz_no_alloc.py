@@ -25,7 +25,7 @@ def case(dev):
     return experts, shared, DeviceExperts(experts, dev), DeviceExperts([shared], dev)
 
 
-def _run(ops, dev, case, x, logits, static):
+def _run(ops, dev, case, x, logits, static, rows_max=ROWS_MAX):
     experts, shared, de, ds = case
     rows = x.shape[0]
     sel = torch.full((rows, TOPK), -1, dtype=torch.int64, device=dev)
@@ -35,9 +35,9 @@ def _run(ops, dev, case, x, logits, static):
               shared_bits=4)
     xt = to_dev(x, dev).to(torch.bfloat16)
     if static:
-        ops.moe_forward_static(ops.MoeShape(ROWS_MAX, H, I, TOPK, E, 1, 0, 0), xt, de.table, out, **kw)
+        ops.moe_forward_static(ops.MoeShape(rows_max, H, I, TOPK, E, 1, 0, 0), xt, de.table, out, **kw)
     else:
-        ws = ops.MoeWorkspace(dev, rows_max=ROWS_MAX, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True)
+        ws = ops.MoeWorkspace(dev, rows_max=rows_max, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True)
         ws.buffer.fill_(0x7f)
         ws.clear_flags()
         ops.moe_forward(ws, xt, de.table, out, **kw)
@@ -54,6 +54,26 @@ def test_static_scratch_matches_workspace_twice(dev, case):
         logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
         got = _run(ops, dev, case, x, logits, static=True)
         want = _run(ops, dev, case, x, logits, static=False)
+        for g, w in zip(got, want):
+            assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
+                                  w.view(np.uint32) if w.dtype == np.float32 else w), (n, rows)
+        ref, ridx, _, _ = coop.moe_layer(x, logits, experts, shared, TOPK, 0.75)
+        assert np.array_equal(got[1], ridx)
+        assert rel_err_rows(got[0], ref) < 1e-2
+
+
+def test_static_scratch_past_16_rows(dev, case):
+    """Past 16 rows the workspace path pipelines its two tile size classes on the thread's side
+    stream, while the fixed-scratch entry point creates no stream and runs every stage on the
+    caller's: both give the same bits, at 40 rows and then 20 (both calls on the MFMA path)."""
+    from eva_amd import ops
+    experts, shared, _, _ = case
+    rng = np.random.default_rng(810)
+    for n, rows in enumerate((40, 20)):
+        x = synth.activations_bf16(rng, rows, H)
+        logits = synth.logits_skewed(rng, rows, E, hot=1, warm=3)
+        got = _run(ops, dev, case, x, logits, static=True, rows_max=40)
+        want = _run(ops, dev, case, x, logits, static=False, rows_max=40)
         for g, w in zip(got, want):
             assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
                                   w.view(np.uint32) if w.dtype == np.float32 else w), (n, rows)
