@@ -45,17 +45,18 @@ __device__ __forceinline__ void mfma_item_rows(const uint32_t* trellis, int nt_n
                                                const GlobalRows& src, const int* slot_of, int rows, float* part,
                                                size_t part_stride, uint32_t* lds)
 {
-    // equal-length items of one 16-row block (calls of at most 16 tokens) gain from progress
-    // priorities (3 waves per SIMD); the prefill kernel's items differ in rows and gain nothing
+    // both kernels run their items with progress priorities: the 16-row kernel's equal items,
+    // and the 64-row kernel's items of 1-4 row blocks since they share the GPU with the 16-row
+    // kernel on another stream (512 tokens: gate/up 1319-1331 -> 1268-1287 us)
     if constexpr (MBMAX == 1) {
         mfma_item<K2, 1, true>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds);
     } else {
         const int mb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
         switch (mb) {
-            case 1: mfma_item<K2, 1, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-            case 2: mfma_item<K2, 2, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-            case 3: mfma_item<K2, 3, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-            default: mfma_item<K2, 4, false>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 1: mfma_item<K2, 1, true>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 2: mfma_item<K2, 2, true>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            case 3: mfma_item<K2, 3, true>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
+            default: mfma_item<K2, 4, true>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
         }
     }
 }
