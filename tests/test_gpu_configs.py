@@ -123,6 +123,38 @@ def test_prefill_forms_bit_identical(dev, T, zipf):
     assert rel_err_rows(outs[1], ref) < TOL
 
 
+@pytest.mark.parametrize("T,E,shared", [(24, 64, False), (64, 4, True)])
+def test_prefill_one_size_class_empty(dev, T, E, shared):
+    """Calls of more than 16 tokens whose tiles fall in one size class only: 24 tokens over 64
+    experts with no shared expert (every tile at most 16 rows: the 64-row kernels and the larger
+    class's activation have no work), 64 tokens over 4 experts and the shared one (every tile
+    64 rows: the side stream's kernels have none). Bit-identical to the single-stream form and
+    within the tolerance of the oracle."""
+    import os
+    from eva_amd import ops
+    H, I, topk = 512, 256, 2
+    rng = np.random.default_rng(300 + T)
+    experts = [synth.expert(rng, H, I, 4, 1 / np.sqrt(H)) for _ in range(E)]
+    sh = synth.expert(rng, H, I, 4, 1 / np.sqrt(H)) if shared else None
+    x = synth.activations_bf16(rng, T, H)
+    logits = synth.logits_plain(rng, T, E)
+    de = DeviceExperts(experts, dev)
+    ds = DeviceExperts([sh], dev) if shared else None
+    outs = []
+    for env in ({}, {"EVAMX_PREFILL_CONCURRENT": "0"}):
+        os.environ.update(env)
+        try:
+            out, sel = _moe(ops, dev, H, I, E, topk, T, de.table, de.k2, to_dev(x, dev).to(torch.bfloat16),
+                            to_dev(logits, dev), ds.ptrs(0) if shared else None, 4.0 if shared else None, limit=CLIP)
+        finally:
+            for key in env:
+                os.environ.pop(key, None)
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    ref = coop.moe_layer(x, logits, experts, sh, topk, CLIP)[0]
+    assert rel_err_rows(outs[0], ref) < TOL
+
+
 class _DeviceRandomExperts:
     """E experts at per-expert rates, drawn on the device (seeded), with a [9, E] pointer table."""
 
