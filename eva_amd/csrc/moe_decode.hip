@@ -1990,65 +1990,79 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
 }
 
 // The same reduction for large batches, where throughput matters more than the latency of one
-// token: one wave per (token, 128 columns) walks the token's items in slot order (shared expert
-// last), issuing the loads of COMBINE_BATCH items together. Same operations in the same order as
-// moe_combine_kernel, so the two give identical results.
+// token: one wave per (token, CGW groups of 128 columns) walks the token's items in slot order
+// (shared expert last), COMBINE_BATCH items at a time: it reads their metadata (local expert,
+// split count, weight, svh pointer) once for its CGW column groups, then for each column group
+// issues the items' loads together and adds them in slot order. Same operations in the same order
+// per column as moe_combine_kernel, so the two give identical results.
 constexpr int COMBINE_BATCH = 4;
 
+template <int CGW>
 __global__ __launch_bounds__(256) void moe_combine_rows_kernel(MoeParams p)
 {
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6));
-    const int ncg = p.H / 128;
-    if (wid >= p.T * ncg) return;
-    const int row = wid / ncg, cg = wid - row * ncg;
+    const int ngw = p.H / 128 / CGW;                 // column-group blocks per token (CGW divides H/128)
+    if (wid >= p.T * ngw) return;
+    const int row = wid / ngw, cg0 = (wid - row * ngw) * CGW;
     const int slots = p.T * p.topk;
     const KSplit kd = ks_down(p, __builtin_amdgcn_readfirstlane(p.meta[2]));
-    const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
     const int nitems = p.topk + (p.has_shared ? 1 : 0);
-    float o0 = 0.0f, o1 = 0.0f;
+    float o[CGW][2];
+#pragma unroll
+    for (int c = 0; c < CGW; ++c) o[c][0] = o[c][1] = 0.0f;
     for (int b = 0; b < nitems; b += COMBINE_BATCH) {
         int sk[COMBINE_BATCH], le[COMBINE_BATCH], S[COMBINE_BATCH];
-        float w[COMBINE_BATCH], v[COMBINE_BATCH][2], sv[COMBINE_BATCH][2];
+        float w[COMBINE_BATCH];
+        const half_t* svh[COMBINE_BATCH];
 #pragma unroll
         for (int j = 0; j < COMBINE_BATCH; ++j) {
             const int k = b + j;
             const bool shared = k == p.topk;
             sk[j] = shared ? slots + row : row * p.topk + k;
             le[j] = -2;                                   // -2: past the items
+            svh[j] = nullptr;
             if (k < nitems) {
                 le[j] = shared ? -1 : __builtin_amdgcn_readfirstlane(p.local[sk[j]]);
                 S[j] = ks_of_chunk(kd, __builtin_amdgcn_readfirstlane(p.slot_mult[sk[j]]));
                 w[j] = shared ? 1.0f : h2f(p.rw16[sk[j]]);
+                if (le[j] >= 0 || (shared && le[j] == -1))
+                    svh[j] = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
+                                    : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le[j]];
             }
         }
 #pragma unroll
-        for (int j = 0; j < COMBINE_BATCH; ++j) {
-            const bool shared = b + j == p.topk;
-            if (le[j] >= 0 || (shared && le[j] == -1)) {
-                const half_t* svh = shared ? (const half_t*)p.sh_ptr[EVAMX_TBL_D_SVH]
-                                           : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le[j]];
-                sum_partials(p, sk[j], cg, lane, S[j], v[j]);
-                sv[j][0] = h2f(svh[col0]);
-                sv[j][1] = h2f(svh[col1]);
-            }
-        }
+        for (int c = 0; c < CGW; ++c) {
+            const int cg = cg0 + c;
+            const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
+            float v[COMBINE_BATCH][2], sv[COMBINE_BATCH][2];
 #pragma unroll
-        for (int j = 0; j < COMBINE_BATCH; ++j) {
-            const bool shared = b + j == p.topk;
-            if (le[j] >= 0 || (shared && le[j] == -1)) {
-                combine_item(shared, w[j], sv[j][0], sv[j][1], v[j], lane);
-                if (shared && p.sh_gate_w) {
-                    const float gv = p.gate_val[row];
-                    v[j][0] = gv * v[j][0];
-                    v[j][1] = gv * v[j][1];
+            for (int j = 0; j < COMBINE_BATCH; ++j) {
+                if (svh[j]) {
+                    sum_partials(p, sk[j], cg, lane, S[j], v[j]);
+                    sv[j][0] = h2f(svh[j][col0]);
+                    sv[j][1] = h2f(svh[j][col1]);
                 }
-                o0 = o0 + v[j][0];
-                o1 = o1 + v[j][1];
+            }
+#pragma unroll
+            for (int j = 0; j < COMBINE_BATCH; ++j) {
+                if (svh[j]) {
+                    const bool shared = b + j == p.topk;
+                    combine_item(shared, w[j], sv[j][0], sv[j][1], v[j], lane);
+                    if (shared && p.sh_gate_w) {
+                        const float gv = p.gate_val[row];
+                        v[j][0] = gv * v[j][0];
+                        v[j][1] = gv * v[j][1];
+                    }
+                    o[c][0] = o[c][0] + v[j][0];
+                    o[c][1] = o[c][1] + v[j][1];
+                }
             }
         }
     }
-    combine_store(p, row, col0, col1, o0, o1);
+#pragma unroll
+    for (int c = 0; c < CGW; ++c)
+        combine_store(p, row, (cg0 + c) * 128 + lane_col(lane, 0), (cg0 + c) * 128 + lane_col(lane, 1), o[c][0], o[c][1]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2192,7 +2206,11 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         else
             launch_timed(moe_combine_kernel<false>, dim3(p.T * (p.H / 128)), dim3(64 * nw), stream, ev(8), ev(9), p);
     } else {
-        launch_timed(moe_combine_rows_kernel, dim3((p.T * (p.H / 128) + 3) / 4), dim3(256), stream, ev(8), ev(9), p);
+        // two column groups per wave: 512 tokens 90.6 -> 88.1 us (four: 100 us, too few waves)
+        if ((p.H / 128) % 2 == 0)
+            launch_timed(moe_combine_rows_kernel<2>, dim3((p.T * (p.H / 256) + 3) / 4), dim3(256), stream, ev(8), ev(9), p);
+        else
+            launch_timed(moe_combine_rows_kernel<1>, dim3((p.T * (p.H / 128) + 3) / 4), dim3(256), stream, ev(8), ev(9), p);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
