@@ -1821,8 +1821,6 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     }
 }
 
-// Activation launch: one wave per (row, chunk) for small batches (latency), per (row, 4 chunks)
-// for large ones (the row's slot, expert and pointers resolved once).
 // The activation stage for the rows of one size class of MFMA tiles (cls 1: tiles of at most 16
 // rows, cls 2: larger), calls of more than 16 tokens.
 static void launch_act_class(const MoeParams& p, int cls, hipStream_t stream)
@@ -1840,6 +1838,8 @@ static void launch_act_class(const MoeParams& p, int cls, hipStream_t stream)
     }
 }
 
+// Activation launch: one wave per (row, chunk) for small batches (latency), per (row, 4 chunks)
+// for large ones (the row's slot, expert and pointers resolved once).
 static void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
 {
     const int na = p.I / 128;
