@@ -76,7 +76,7 @@ __device__ __forceinline__ int xcd_item_block(int b, int nb)
 // Every tile is one work unit of weight 1; the k-split is the decode GEMV's (moe_ksplit: as many
 // splits as fill the resident grid once, or the requested count), so the activation and combine
 // kernels sum the same partials. MBMAX bounds the tile rows in 16-row blocks: the MBMAX 1 kernel
-// (a quarter of the accumulators, 3 waves per SIMD) runs the tiles of at most 16 rows, the
+// (a quarter of the accumulators, 4 waves per SIMD) runs the tiles of at most 16 rows, the
 // MBMAX 4 kernel the larger ones; the split count is the same for both (from all the tiles).
 template <int MBMAX, int which>
 __device__ __forceinline__ void mfma_stage(const MoeParams& p, uint32_t (&lds)[MF_WAVES][MF_LDS_WORDS])
@@ -88,9 +88,10 @@ __device__ __forceinline__ void mfma_stage(const MoeParams& p, uint32_t (&lds)[M
     const KSplit k = which == 0 ? ks_gate_up(p, n_all) : ks_down(p, n_all);
     const int S = ks_of_chunk(k, 1);
     const int per_tile = (which == 0 ? 2 * ncg : ncg) * S;
-    // this launch's tiles: the small ones (at most 16 rows) in the MBMAX 1 kernel when they fill
-    // at least three of its resident rounds (3 waves per SIMD), so that its last round's tail is
-    // short; the rest (or all) in the MBMAX 4 kernel. Up to 16 tokens every tile is small.
+    // this launch's tiles: the small ones (at most 16 rows) in the MBMAX 1 kernel when the two
+    // kernels run on two streams (force_split), or, on one stream, when they fill at least three
+    // rounds of three waves per SIMD, so that its last round's tail is short; the rest (or all) in
+    // the MBMAX 4 kernel. Up to 16 tokens every tile is small.
     const bool split = p.force_split || p.T <= EVAMX_SMALL_TILE_ROWS || (long)n_small * per_tile >= 3L * (p.gemv_waves * 3 / 4);
     const int n_tiles = MBMAX == 1 ? (split ? n_small : 0) : (split ? n_all - n_small : n_all);
     // the call's items fill the first n_blk workgroups (a multiple of 8, spread over the XCDs)
@@ -381,7 +382,7 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     const int kmax = which == 0 ? p.ks_gu_max : p.ks_d_max;
     const long per_tile = (long)(which == 0 ? 2 * ncg : ncg);
     const long items = mfma_items(p, which);
-    // tiles of at most 16 rows run in the 16-row kernel (3 waves per SIMD, progress priorities),
+    // tiles of at most 16 rows run in the 16-row kernel (4 waves per SIMD, progress priorities),
     // larger ones in the 64-row kernel; up to 16 tokens every tile is a small one
     // The small-tile launch is skipped when the split can never happen: at most one tile per
     // expert (its remainder) and one shared tile are small, at the largest split count
