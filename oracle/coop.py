@@ -384,10 +384,13 @@ def moe_layer(x, logits, experts, shared, topk, limit, score_fn="sigmoid", sel_b
 
 
 def round_bf16(v):
-    """fp32 -> nearest bf16 (ties to even), returned as float32 values."""
+    """fp32 -> nearest bf16 (ties to even; overflow to +-inf), returned as float32 values.
+    A NaN stays a NaN (quieted), as torch's ``.to(torch.bfloat16)`` keeps it."""
     x = np.ascontiguousarray(np.asarray(v, dtype=np.float32))
     u = x.view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = np.where(nan, ((u >> 16) | 0x40) << 16, r)
     return r.astype(np.uint32).view(np.float32)
 
 

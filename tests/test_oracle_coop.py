@@ -292,3 +292,68 @@ def test_clamp_orders_separate_at_the_test_limit(rows):
     # and the limit of 10 used elsewhere never engages at these scales
     v10 = clamp_variants(lambda: coop.moe_layer(x, logits, experts, shared, topk, 10.0)[0])
     assert np.array_equal(v10["unclamped"], v10["ref"])
+
+
+# ---------------------------------------------------------------------------------------------
+# bf16 residual stream: the oracle's helpers against torch's own fp32 -> bf16 cast
+# and bf16 add, the operations of model.py:498-499 (``y.to(x.dtype)`` then ``h + y``).
+
+
+def _bf16_probe_values():
+    rng = np.random.default_rng(41)
+    u = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    hi = rng.integers(0, 2**16, size=1 << 16, dtype=np.uint64).astype(np.uint32) << 16
+    special = [
+        hi | 0x8000,                                   # exact ties, even and odd bf16 neighbours
+        hi | 0x7FFF, hi | 0x8001,                      # one below / above a tie
+        np.arange(0, 1 << 16, dtype=np.uint32) * 131,  # fp32 subnormals and tiny normals
+        np.arange(0x7F7F0000, 0x7F800000, 7, dtype=np.uint32),   # near the overflow edge
+        np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x00800000, 0x807FFFFF], np.uint32),
+    ]
+    v = np.concatenate([u, *special]).astype(np.uint32)
+    for s in (0, 0x80000000):
+        v = np.concatenate([v, v[: 1 << 16] ^ s])
+    v = v[(v & 0x7FFFFFFF) <= 0x7F800000]              # finite and +-inf; NaN checked apart
+    return v.view(np.float32)
+
+
+def test_round_bf16_matches_torch_cast():
+    torch = pytest.importorskip("torch")
+    x = _bf16_probe_values()
+    assert x.size >= 1_000_000
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = coop.round_bf16(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    nans = np.array([0x7FC00000, 0xFFC00001, 0x7F800001, 0x7FBFFFFF], np.uint32).view(np.float32)
+    assert np.isnan(coop.round_bf16(nans)).all()
+    assert np.isnan(torch.from_numpy(nans).to(torch.bfloat16).float().numpy()).all()
+
+
+def test_residual_add_matches_torch_bf16_add():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(42)
+    n = 1 << 19
+    h = torch.from_numpy(rng.standard_normal(n).astype(np.float32) * 4).to(torch.bfloat16)
+    y = rng.standard_normal(n).astype(np.float32) * np.float32(2.0) ** rng.integers(-12, 6, n).astype(np.float32)
+    # ties of the final rounding: y a bf16 value that lands h + y exactly between neighbours
+    y[:4096] = (h[:4096].float().numpy().view(np.uint32) & 0xFFFF0000).view(np.float32) * np.float32(2.0**-8)
+    want = (h + torch.from_numpy(y).to(torch.bfloat16)).float().numpy()
+    got = coop.residual_add(h.float().numpy(), y)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_layer_stack_one_layer_is_residual_add_of_the_layer():
+    H, I, E, topk, K = 256, 128, 6, 2, 3
+    rng = np.random.default_rng(43)
+    experts = [synth.expert(rng, H, I, K, 1 / np.sqrt(H)) for _ in range(E)]
+    shared = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
+    h = coop.round_bf16(rng.standard_normal((3, H)).astype(np.float32))
+    logits = [synth.logits_plain(rng, 3, E)]
+    got = coop.layer_stack(h, logits, [(experts, shared)], topk, 10.0)
+    y = coop.moe_layer(h, logits[0], experts, shared, topk, 10.0)[0]
+    assert np.array_equal(got, coop.residual_add(h, y))
+    # two layers: the second layer routes on its own logits and reads the first's output
+    logits2 = logits + [synth.logits_plain(rng, 3, E)]
+    got2 = coop.layer_stack(h, logits2, [(experts, shared)] * 2, topk, 10.0)
+    y2 = coop.moe_layer(got, logits2[1], experts, shared, topk, 10.0)[0]
+    assert np.array_equal(got2, coop.residual_add(got, y2))
