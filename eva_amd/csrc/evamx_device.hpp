@@ -176,49 +176,6 @@ __device__ __forceinline__ half2_t half_hpair(const uint32_t (&N)[B + 1])
 }
 
 // ---------------------------------------------------------------------------------------------
-// Table-assisted decode: the (1024 + bytesum) fp16 value of every 16-bit state, in LDS
-// (65 536 entries, 128 KiB; entry x is mul1_hpair's value for state x), replaces the two
-// multiplies and the byte sum of a weight by one LDS read. Same windows as lane_hash/half_hash.
-
-typedef const __attribute__((address_space(3))) uint16_t* mul1_tab_t;
-
-template <int K, int J>
-__device__ __forceinline__ uint32_t lane_tval(const LaneWords<K>& w, mul1_tab_t tab)
-{
-    constexpr int E = win_end<K>(J);
-    if constexpr (16 % K == 0) {
-        constexpr int P = 16 / K;
-        if constexpr ((J / P) % 2 == 0)
-            return tab[win_reg<K, E + 16>(w) >> 16];
-        else
-            return tab[win_reg<K, E>(w) & 0xffffu];
-    } else {
-        return tab[win_reg<K, E>(w) & 0xffffu];
-    }
-}
-
-template <int K, int J>
-__device__ __forceinline__ half2_t lane_tpair(const LaneWords<K>& w, mul1_tab_t tab)
-{
-    return __builtin_bit_cast(half2_t, lane_tval<K, J>(w, tab) | (lane_tval<K, J + 1>(w, tab) << 16));
-}
-
-template <int B, int J>
-__device__ __forceinline__ uint32_t half_tval(const uint32_t (&N)[B + 1], mul1_tab_t tab)
-{
-    constexpr int E = half_win_end<B>(J);
-    constexpr int L = (E - 1) / 32;
-    constexpr int S = 32 * (L + 1) - E;
-    return tab[funnel(N[L > 0 ? L - 1 : 0], N[L], S) & 0xffffu];
-}
-
-template <int B, int J>
-__device__ __forceinline__ half2_t half_tpair(const uint32_t (&N)[B + 1], mul1_tab_t tab)
-{
-    return __builtin_bit_cast(half2_t, half_tval<B, J>(N, tab) | (half_tval<B, J + 1>(N, tab) << 16));
-}
-
-// ---------------------------------------------------------------------------------------------
 // Wave-level 128-point Hadamard in the reference's fp32 evaluation order: radix-2 on element
 // bits 0..6 in increasing order, lower index a+b, upper a-b, scale last. Bit-identical to the
 // reference for any data layout, because IEEE addition is commutative and each stage's

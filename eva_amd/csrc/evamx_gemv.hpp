@@ -199,54 +199,6 @@ __device__ __forceinline__ void decode_slice(const LaneWords<Rate<K2>::K>& w, ui
     }
 }
 
-// The same pairs with the pairs whose bit is set in MASK decoded through the LDS table.
-template <int K2, uint32_t MASK>
-__device__ __forceinline__ void decode_slice_tab(const LaneWords<Rate<K2>::K>& w, uint32_t sh, half2_t (&wp)[16],
-                                                 mul1_tab_t tab)
-{
-    using R = Rate<K2>;
-    constexpr int K = R::K, B = R::B;
-    if constexpr (!R::HALF) {
-#define EVAMX_DEC_PAIR(P) \
-        wp[P] = ((MASK >> (P)) & 1) ? lane_tpair<K, 2 * (P)>(w, tab) : lane_hpair<K, 2 * (P)>(w);
-        EVAMX_DEC_PAIR(0) EVAMX_DEC_PAIR(1) EVAMX_DEC_PAIR(2) EVAMX_DEC_PAIR(3)
-        EVAMX_DEC_PAIR(4) EVAMX_DEC_PAIR(5) EVAMX_DEC_PAIR(6) EVAMX_DEC_PAIR(7)
-        EVAMX_DEC_PAIR(8) EVAMX_DEC_PAIR(9) EVAMX_DEC_PAIR(10) EVAMX_DEC_PAIR(11)
-        EVAMX_DEC_PAIR(12) EVAMX_DEC_PAIR(13) EVAMX_DEC_PAIR(14) EVAMX_DEC_PAIR(15)
-#undef EVAMX_DEC_PAIR
-    } else {
-        uint32_t N[B + 1];
-#pragma unroll
-        for (int k = 0; k <= B; ++k) N[k] = __builtin_amdgcn_alignbit(w.b[k], w.b[k + 1], sh);
-#define EVAMX_DEC_PAIR(P) \
-        wp[P] = ((MASK >> (P)) & 1) ? half_tpair<B, 2 * (P)>(N, tab) : half_hpair<B, 2 * (P)>(N);
-        EVAMX_DEC_PAIR(0) EVAMX_DEC_PAIR(1) EVAMX_DEC_PAIR(2) EVAMX_DEC_PAIR(3)
-        EVAMX_DEC_PAIR(4) EVAMX_DEC_PAIR(5) EVAMX_DEC_PAIR(6) EVAMX_DEC_PAIR(7)
-        EVAMX_DEC_PAIR(8) EVAMX_DEC_PAIR(9) EVAMX_DEC_PAIR(10) EVAMX_DEC_PAIR(11)
-        EVAMX_DEC_PAIR(12) EVAMX_DEC_PAIR(13) EVAMX_DEC_PAIR(14) EVAMX_DEC_PAIR(15)
-#undef EVAMX_DEC_PAIR
-    }
-}
-
-// Decoders of gemv_wave: every pair on the vector ALU, or the MASK pairs through the LDS table.
-struct ValuDec {
-    template <int K2>
-    __device__ __forceinline__ void slice(const LaneWords<Rate<K2>::K>& w, uint32_t sh, half2_t (&wp)[16]) const
-    {
-        decode_slice<K2>(w, sh, wp);
-    }
-};
-
-template <uint32_t MASK>
-struct TabDec {
-    mul1_tab_t tab;
-    template <int K2>
-    __device__ __forceinline__ void slice(const LaneWords<Rate<K2>::K>& w, uint32_t sh, half2_t (&wp)[16]) const
-    {
-        decode_slice_tab<K2, MASK>(w, sh, wp, tab);
-    }
-};
-
 // ---------------------------------------------------------------------------------------------
 // Activation rows of a GEMV chunk: row m holds the k-vector of slot slot_of[m], read through
 // wave-uniform addresses (scalar loads), together with its per-128-chunk sums (fp32) that the
@@ -322,10 +274,9 @@ struct NoPrologue {
 template <int TM>
 constexpr int prefetch_depth() { return 4; }
 
-template <int K2, int TM, int PF = prefetch_depth<TM>(), typename XS, typename Pro, typename Dec = ValuDec>
+template <int K2, int TM, int PF = prefetch_depth<TM>(), typename XS, typename Pro>
 __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
-                                          const XS& xs, int tm, float (&acc)[TM][2], Pro& prologue,
-                                          const Dec& dec = Dec())
+                                          const XS& xs, int tm, float (&acc)[TM][2], Pro& prologue)
 {
     using R = Rate<K2>;
     constexpr int K = R::K;
@@ -371,7 +322,7 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
         half2_t xn[TM][8];
         if constexpr (XPF) load_x(xn, min(kt + 1, last));
         half2_t wp[16];
-        dec.template slice<K2>(w, sh, wp);
+        decode_slice<K2>(w, sh, wp);
         load_slice<K>(w, rsrc, cbase + (uint32_t)min(kt + PF, last) * slice, lane_off, prev_off);
 #pragma unroll
         for (int m = 0; m < TM; ++m) {

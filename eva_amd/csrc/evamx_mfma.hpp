@@ -153,175 +153,6 @@ __device__ __forceinline__ void mfma_row_sums(const GlobalRows& src, const int* 
         for (int r = 0; r < 4; ++r) xs[mb][r] = __shfl(v[mb], 4 * g + r, WAVE);
 }
 
-// ---------------------------------------------------------------------------------------------
-// Workgroup-cooperative form, for calls of more than 16 tokens. The four waves of a workgroup
-// share one work item (tile of <= 64 rows, 128 columns, k-range), in stages of four k-slices
-// (two MFMA k-steps):
-//
-//   - at stage st, wave w decodes k-slice kt0 + 4 st + w of the item's 8 trellis tiles (the
-//     decode layout above) into its quarter of the stage's B operands in LDS (k-slice 4 st + w
-//     is half s = w & 1 of k-step w >> 1);
-//   - the workgroup's 256 lanes load the stage's A operands (the tile's rows, 64 k) once, 16 B
-//     each, four stages ahead like the weights, and write them into LDS at the stage;
-//   - after one workgroup barrier every wave runs the MFMAs of its own 32 columns (B operands
-//     2w, 2w + 1) over the stage's two k-steps for all the tile's 16-row blocks;
-//   - stages alternate between two LDS buffers, so one barrier per stage orders a stage's writes
-//     before its reads and the reads of stage st before the writes of stage st + 2.
-//
-// Vector memory loads complete in order, so a wait for one load is a wait for every load issued
-// before it: the A loads of stage st are issued just before the weight loads of the same stage
-// and waited for at stage st, so they never make a wave wait for weights it does not need yet.
-//
-// Each weight is decoded once per tile, as in the single-wave form, but a wave holds a quarter
-// of its accumulators (8 MB registers), so three waves fit per SIMD, and a workgroup finishes an
-// item four times sooner, so the grid's last round is short.
-constexpr int MFW_STAGE_WORDS = 2 * 8 * 64 * 4;   // B of one stage: 2 k-steps x 8 operands x 64 lanes x 16 B
-constexpr int MFW_A_WORDS = 2 * 4 * 64 * 4;       // A of one stage: 2 k-steps x 4 row blocks x 64 lanes x 16 B
-constexpr int MFW_LDS_WORDS = 2 * (MFW_STAGE_WORDS + MFW_A_WORDS);   // two stages (48 KiB)
-
-template <int K2, int MB>
-__device__ __forceinline__ void mfma_accumulate_wg(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
-                                                   const GlobalRows& src, const int* __restrict__ slot_of, int rows,
-                                                   uint32_t* lds, f32x4_t (&acc)[MB][2])
-{
-    using R = Rate<K2>;
-    constexpr int K = R::K;
-    constexpr int TW = R::TW;
-    constexpr int AR = MB > 2 ? 2 : 1;             // A load rounds per stage (128 lanes per row block)
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int q = lane & 7, ti = lane >> 3;       // decode layout: run q of tile ti
-    kt0 = __builtin_amdgcn_readfirstlane(kt0);
-    const int nst = (__builtin_amdgcn_readfirstlane(kt1) - kt0) >> 2;   // even: k-ranges are whole 128-chunks
-    const uint32_t slice = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(nt_n * TW));
-    const uint32_t sstep = 4u * slice;
-    const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW) +
-                                                          (uint32_t)(kt0 + wave) * slice);
-    const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(trellis);
-    uint32_t lane_off, prev_off, sh;
-    lane_offsets<K2>(lane, lane_off, prev_off, sh);
-
-    // A loader: lane (m16, g) of wave w loads row 16 mb + m16, k-step h = w & 1, k group g, with
-    // mb = w >> 1 in round 0 and 2 + (w >> 1) in round 1 (rows past the tile read row 0; their
-    // results are dropped), and stores it at u32x4 index 256 h + 64 mb + lane of the stage's A
-    const int ah = wave & 1, amb = wave >> 1;
-    const int m16 = lane & 15, g = lane >> 4;
-    const __attribute__((address_space(1))) u32x4_t* arow[AR];
-#pragma unroll
-    for (int r = 0; r < AR; ++r) {
-        const int row = 16 * (amb + 2 * r) + m16;
-        const int s = slot_of[row < rows ? row : 0];
-        arow[r] = (const __attribute__((address_space(1))) u32x4_t*)(src.A + (size_t)s * src.stride + 16 * kt0) + 4 * ah + g;
-    }
-    auto a_valid = [&](int r) { return amb + 2 * r < MB; };
-
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[mb][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // prefetch: stage d's A loads, then its weights (the order every later stage keeps)
-    LaneWords<K> ring[MF_PF];
-    u32x4_t aring[MF_PF][AR];
-    const int last = nst - 1;
-#pragma unroll
-    for (int d = 0; d < MF_PF; ++d) {
-        const int sd = min(d, last);
-#pragma unroll
-        for (int r = 0; r < AR; ++r)
-            if (a_valid(r)) aring[d][r] = arow[r][8 * sd];
-        load_slice<K>(ring[d], rsrc, cbase + (uint32_t)sd * sstep, lane_off, prev_off);
-    }
-
-    // LDS: B operand nb of k-step h at u32x4 index 512 h + 64 nb + (n + 16 g'), n = 8c + q the
-    // column and g' = 2s + kh the k group; A of row block mb, k-step h at 256 h + 64 mb + lane
-    uint32_t* bw = lds + 4 * (512 * (wave >> 1) + 64 * ti + q + 32 * (wave & 1));
-    const uint32_t* br = lds + 4 * (64 * 2 * wave + lane);
-    uint32_t* aw = lds + 2 * MFW_STAGE_WORDS + 4 * (256 * ah + 64 * amb + lane);
-    const uint32_t* ar = lds + 2 * MFW_STAGE_WORDS + 4 * lane;
-
-    auto stage = [&](int st, LaneWords<K>& w, u32x4_t (&a)[AR]) {
-        const int bbuf = (st & 1) * MFW_STAGE_WORDS;
-        const int abuf = (st & 1) * MFW_A_WORDS;
-        // this stage's A (loaded four stages ago) into LDS, then the loads of stage st + 4
-#pragma unroll
-        for (int r = 0; r < AR; ++r)
-            if (a_valid(r)) *(u32x4_t*)(aw + abuf + 4 * 128 * r) = a[r];
-        const int sn = min(st + MF_PF, last);
-#pragma unroll
-        for (int r = 0; r < AR; ++r)
-            if (a_valid(r)) a[r] = arow[r][8 * sn];
-        half2_t wp[16];
-        decode_slice<K2>(w, sh, wp);
-        load_slice<K>(w, rsrc, cbase + (uint32_t)sn * sstep, lane_off, prev_off);
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                const u32x4_t v = {__builtin_bit_cast(uint32_t, wp[kh + 2 * c]),
-                                   __builtin_bit_cast(uint32_t, wp[kh + 2 * c + 4]),
-                                   __builtin_bit_cast(uint32_t, wp[kh + 2 * c + 8]),
-                                   __builtin_bit_cast(uint32_t, wp[kh + 2 * c + 12])};
-                *(u32x4_t*)(bw + bbuf + 4 * (8 * c + 16 * kh)) = v;
-            }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            u32x4_t av[MB];
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) av[mb] = *(const u32x4_t*)(ar + abuf + 4 * (256 * h + 64 * mb));
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const u32x4_t bv = *(const u32x4_t*)(br + bbuf + 4 * (512 * h + 64 * j));
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-                    acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av[mb]),
-                                                                        __builtin_bit_cast(half8_t, bv), acc[mb][j], 0, 0, 0);
-            }
-        }
-    };
-
-    // the rings' four slots take four stages per round; nst is even, so a round may end after two
-    for (int st = 0; st < nst; st += 4) {
-        stage(st, ring[0], aring[0]);
-        stage(st + 1, ring[1], aring[1]);
-        if (st + 2 < nst) {
-            stage(st + 2, ring[2], aring[2]);
-            stage(st + 3, ring[3], aring[3]);
-        }
-    }
-}
-
-// One work item of the cooperative form with its partials stored: wave w writes columns
-// 32 w .. 32 w + 31 of part[slot * part_stride + 128 * cg + column] for rows < rows.
-template <int K2, int MB>
-__device__ __forceinline__ void mfma_item_wg(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
-                                             const GlobalRows& src, const int* __restrict__ slot_of, int rows,
-                                             float* __restrict__ part, size_t part_stride, uint32_t* lds)
-{
-    f32x4_t acc[MB][2];
-    mfma_accumulate_wg<K2, MB>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, lds, acc);
-    kt0 = __builtin_amdgcn_readfirstlane(kt0);
-    const int nk = __builtin_amdgcn_readfirstlane(kt1) - kt0;
-    float xs[MB][4];
-    mfma_row_sums<MB>(src, slot_of, rows, kt0, nk, xs);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int m16 = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * mb + 4 * g + r;
-            if (row < rows) {
-                float* dst = part + (size_t)slot_of[row] * part_stride + 128 * cg + 32 * wave + m16;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) dst[16 * j] = MUL1_K_INV * acc[mb][j][r] + MUL1_K_BIAS * xs[mb][r];
-            }
-        }
-    }
-}
-
 // One work item with its partials stored: part[slot * part_stride + 128 * cg + column] =
 // 0x1eee * acc + 0xc931 * (row's activation sum), for rows < rows.
 template <int K2, int MB, bool PRIO>

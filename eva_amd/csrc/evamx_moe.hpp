@@ -234,8 +234,6 @@ struct SideStream {
     hipEvent_t fork = nullptr, join = nullptr;
 };
 const SideStream* side_stream(hipStream_t stream);
-// EVAMX_PREFILL_FORM=coop: the opt-in cooperative form of the MFMA stages (moe_prefill.hip).
-bool prefill_coop_form_requested();
 int moe_prepare_only(MoeParams& p, hipStream_t stream);
 int launch_router_logits(const MoeParams& p, float* logits, hipStream_t stream);
 bool moe_small_path(int T, int topk);

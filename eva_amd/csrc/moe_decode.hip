@@ -1199,10 +1199,10 @@ struct RotStageGroup {
 // Gate/up GEMV of tm rows (slots slot[0..tm)) over the 128-chunks [c0, c1): each window of at
 // most ROT_CW chunks is rotated into LDS (GROUP: by the workgroup's four waves together), then
 // streamed; writes the fp32 partials of the rows.
-template <int K2, int TM, bool GROUP, int NW = ROT_WAVES, typename Dec = ValuDec>
+template <int K2, int TM, bool GROUP, int NW = ROT_WAVES>
 __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                  const int (&so)[TM], int tm, int cg, int c0, int c1, float* part,
-                                                 uint32_t* lds, float* lsums, const Dec& dec = Dec())
+                                                 uint32_t* lds, float* lsums)
 {
     const int lane = threadIdx.x & 63;
     float acc[TM][2], xs[TM];
@@ -1223,12 +1223,12 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
             RotStageGroup<TM, NW> stage{p, so, tm, w0, w1, RW, lane, (int)(threadIdx.x >> 6), srs, {}, lds, lsums, xs};
 #pragma unroll
             for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
-            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage, dec);
+            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
         } else {
             RotStage<TM> stage{p, so, tm, w0, w1, RW, lane, srs, {}, lds, xs};
 #pragma unroll
             for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
-            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage, dec);
+            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
         }
     };
     if (c1 - c0 <= ROT_CW) {
@@ -1548,74 +1548,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
             float* dst = part + (size_t)u * p.I + cg * 128;
             dst[lane_col(lane, 0)] = 0.0f;
             dst[lane_col(lane, 1)] = 0.0f;
-        }
-    }
-}
-
-// The same one-row gate/up launch with a table-assisted decode (not the default: see
-// table_decode_requested): workgroups of ROT1T_WAVES waves
-// (one per CU: the table fills 128 KiB of LDS) that share unit, projection and k-split (the
-// column-group count a multiple of 8) and fill the table while their token's routes are being
-// computed; the pairs in ROT1T_MASK of every slice are decoded through it.
-constexpr int ROT1T_WAVES = 8;
-constexpr uint32_t ROT1T_MASK = 0x5b5bu;            // 10 of 16 pairs
-
-__global__ __launch_bounds__(64 * ROT1T_WAVES) void moe_gate_up_route1_tab_kernel(MoeParams p)
-{
-    __shared__ uint32_t tab[32768];
-    __shared__ uint32_t xl[ROT_CW * 64];
-    __shared__ float xsums[ROT_CW];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (blockIdx.x == gridDim.x - 1) {
-        if (wave == 0) publish_routes1(p, lane);
-        return;
-    }
-    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int ncg = p.I / 128;
-    const int S = ks_of_chunk(ks_gate_up(p, p.units_max), 1);
-    const int per_unit = 2 * ncg * S;
-    const int u = __builtin_amdgcn_readfirstlane(wid / per_unit);
-    if (u >= p.units_max) return;                 // whole workgroups (per_unit is a multiple of 8)
-    // the table: entry x = the (1024 + bytesum) fp16 value of state x, two entries per word
-    for (int j = threadIdx.x; j < 32768; j += 64 * ROT1T_WAVES)
-        tab[j] = __builtin_bit_cast(uint32_t, mul1_hpair(mul1_hash<false>(2u * j), mul1_hash<false>(2u * j + 1u)));
-    const int r = wid - u * per_unit;
-    const int cg = __builtin_amdgcn_readfirstlane(r % ncg);
-    const int pk = r / ncg;
-    const int proj = __builtin_amdgcn_readfirstlane(pk / S);
-    const int ks = __builtin_amdgcn_readfirstlane(pk % S);
-    int e = -1;
-    if (u < p.topk) {
-        int id;
-        half_t rw;
-        float w32;
-        slot_routes1(p, lane, id, rw, w32);
-        id = __builtin_amdgcn_readlane(id, u);
-        const half_t rwu = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_readlane((int)__builtin_bit_cast(uint16_t, rw), u));
-        e = __builtin_amdgcn_readfirstlane(slot_local(p, id, rwu, false));
-        if (e < 0) return;                        // the whole workgroup: same unit
-    }
-    const int k2 = __builtin_amdgcn_readfirstlane(k2_gu_of(p, e));
-    const uint32_t* trellis = (const uint32_t*)(proj == 0 ? expert_ptr(p, e, EVAMX_TBL_G_TRELLIS)
-                                                          : expert_ptr(p, e, EVAMX_TBL_U_TRELLIS));
-    const half_t* suh = (const half_t*)(proj == 0 ? expert_ptr(p, e, EVAMX_TBL_G_SUH) : expert_ptr(p, e, EVAMX_TBL_U_SUH));
-    const int nch = p.H / 128;
-    const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
-    float* part = p.part_gu + ((size_t)ks * 2 + proj) * moe_nslot(p) * p.I;
-    const int so[1] = {u};
-    // the table is read after the rotation stage's workgroup barrier
-    const TabDec<ROT1T_MASK> dec{(mul1_tab_t)(const uint16_t*)tab};
-    switch (k2) {
-#define EVAMX_T1(K2V) \
-        case K2V: gate_up_rot_rows<K2V, 1, true, ROT1T_WAVES>(p, trellis, suh, so, 1, cg, c0, c1, part, xl, xsums, dec); break;
-        EVAMX_T1(3) EVAMX_T1(4) EVAMX_T1(5) EVAMX_T1(6) EVAMX_T1(7) EVAMX_T1(8) EVAMX_T1(10)
-#undef EVAMX_T1
-        default: {
-            float* dst = part + (size_t)u * p.I + cg * 128;
-            dst[lane_col(lane, 0)] = 0.0f;
-            dst[lane_col(lane, 1)] = 0.0f;
-            // the other waves of the workgroup meet the rotation barrier: the rate is per unit, so
-            // the whole workgroup takes this branch
         }
     }
 }
@@ -2084,15 +2016,6 @@ int launch_router_logits(const MoeParams& p, float* logits, hipStream_t stream)
 
 bool moe_small_path(int T, int topk) { return T * topk <= EVAMX_SMALL_SLOTS && T <= EVAMX_SMALL_ROWS; }
 
-// The table-assisted decode of one-row gate/up launches is slower on MI355X than the vector-ALU
-// decode (its LDS lookups stall every step), so it runs only when EVAMX_GATE_UP_DECODE=table is
-// set in the environment (read at each call), to reproduce that comparison.
-static bool table_decode_requested()
-{
-    const char* v = getenv("EVAMX_GATE_UP_DECODE");
-    return v && strcmp(v, "table") == 0;
-}
-
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
 {
     // events[2k] / events[2k + 1]: start of the first and end of the last kernel of stage k
@@ -2139,7 +2062,7 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         launch_timed(moe_group_kernel, dim3(1), dim3(64 * GROUP_WAVES), stream, first, nullptr, p);
         launch_timed(moe_rotate_kernel, dim3(EVAMX_ROTATE_BLOCKS), dim3(256), stream, nullptr, ev(1), p);
     }
-    const SideStream* side = p.mfma && p.T > EVAMX_SMALL_TILE_ROWS && p.side_ok && !events && !prefill_coop_form_requested()
+    const SideStream* side = p.mfma && p.T > EVAMX_SMALL_TILE_ROWS && p.side_ok && !events
                                  ? side_stream(stream) : nullptr;
     if (side) {
         // calls of more than 16 tokens: each size class of tiles runs gate/up, activation and
@@ -2176,14 +2099,9 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
             const bool group = (p.I / 128) % ROT_WAVES == 0;
             if (route1) {
                 // one more workgroup publishes the routes and records
-                if ((p.I / 128) % ROT1T_WAVES == 0 && table_decode_requested()) {
-                    const dim3 grid8((unsigned)((waves + ROT1T_WAVES - 1) / ROT1T_WAVES + 1));
-                    launch_timed(moe_gate_up_route1_tab_kernel, grid8, dim3(64 * ROT1T_WAVES), stream, ev(2), ev(3), p);
-                } else {
-                    const dim3 grid1(grid.x + 1);
-                    if (group) launch_timed(moe_gate_up_route1_kernel<true>, grid1, dim3(256), stream, ev(2), ev(3), p);
-                    else launch_timed(moe_gate_up_route1_kernel<false>, grid1, dim3(256), stream, ev(2), ev(3), p);
-                }
+                const dim3 grid1(grid.x + 1);
+                if (group) launch_timed(moe_gate_up_route1_kernel<true>, grid1, dim3(256), stream, ev(2), ev(3), p);
+                else launch_timed(moe_gate_up_route1_kernel<false>, grid1, dim3(256), stream, ev(2), ev(3), p);
             } else if (tmax == 1) {
                 if (group) launch_timed(moe_gate_up_rot_kernel<1, true>, grid, dim3(256), stream, ev(2), ev(3), p);
                 else launch_timed(moe_gate_up_rot_kernel<1, false>, grid, dim3(256), stream, ev(2), ev(3), p);

@@ -24,11 +24,7 @@
 // stream, the larger ones in the 64-row kernel (2 waves per SIMD) on the caller's stream, at the
 // same time; moe_launch pipelines each size class through gate/up, activation and down on its
 // stream (launch_mfma_class), launch_mfma runs one stage's two kernels at once.
-//
-// An opt-in cooperative form (moe_gate_up_wg_kernel / moe_down_wg_kernel, EVAMX_PREFILL_FORM=coop)
-// gives one item to a whole workgroup: its four waves decode a quarter of each stage's k-slices
-// each, stage the A rows once through LDS, and each run the MFMAs of 32 of the 128 columns
-// (mfma_accumulate_wg). Same items, split and partials, bit for bit.
+
 #include <stdlib.h>
 #include <string.h>
 
@@ -160,102 +156,6 @@ __device__ __forceinline__ void mfma_stage(const MoeParams& p, uint32_t (&lds)[M
     }
 }
 
-template <int K2>
-__device__ __forceinline__ void mfma_item_wg_rows(const uint32_t* trellis, int nt_n, int cg, int kt0, int kt1,
-                                                  const GlobalRows& src, const int* slot_of, int rows, float* part,
-                                                  size_t part_stride, uint32_t* lds)
-{
-    const int mb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
-    switch (mb) {
-        case 1: mfma_item_wg<K2, 1>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 2: mfma_item_wg<K2, 2>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 3: mfma_item_wg<K2, 3>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        default: mfma_item_wg<K2, 4>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-    }
-}
-
-// The cooperative form of a projection stage (calls of more than 16 tokens): one item per
-// workgroup, every tile in chunk order (the tiles of one expert run side by side and share its
-// weight reads in L2), consecutive items of a tile on one XCD. Same items, split and partials as
-// mfma_stage.
-template <int which>
-__device__ __forceinline__ void mfma_stage_wg(const MoeParams& p, uint32_t* lds)
-{
-    const int n_all = __builtin_amdgcn_readfirstlane(p.meta[0]);
-    const int ncg = which == 0 ? p.I / 128 : p.H / 128;
-    const KSplit k = which == 0 ? ks_gate_up(p, n_all) : ks_down(p, n_all);
-    const int S = ks_of_chunk(k, 1);
-    const int per_tile = (which == 0 ? 2 * ncg : ncg) * S;
-    const int n_blk = (n_all * per_tile + 7) & ~7;
-    if ((int)blockIdx.x >= n_blk) return;
-    const int item = __builtin_amdgcn_readfirstlane(xcd_item_block(blockIdx.x, n_blk));
-    const int tile = item / per_tile;
-    if (tile >= n_all) return;
-    const int rem = item - tile * per_tile;
-    const int ks = rem % S;
-    const int pc = rem / S;
-    const int proj = which == 0 ? pc / ncg : 2;
-    const int cg = pc - (which == 0 ? proj * ncg : 0);
-    const int* ch = p.chunks + 8 * tile;
-    const int e = __builtin_amdgcn_readfirstlane(ch[0]);
-    const int begin = __builtin_amdgcn_readfirstlane(ch[1]);
-    const int rows = __builtin_amdgcn_readfirstlane(ch[2]);
-    const int k2 = __builtin_amdgcn_readfirstlane(ch[which == 0 ? 3 : 6]);    // gate/up or down rate
-    const int* slot_of = p.order + begin;
-    const int nslot = moe_nslot(p);
-    const int trow = proj == 0 ? EVAMX_TBL_G_TRELLIS : proj == 1 ? EVAMX_TBL_U_TRELLIS : EVAMX_TBL_D_TRELLIS;
-    const uint32_t* trellis = (const uint32_t*)(e < 0 ? (const void*)p.sh_ptr[trow]
-                                                      : (const void*)p.tables[(size_t)trow * p.tbl_stride + e]);
-    GlobalRows src;
-    float* part;
-    size_t part_stride;
-    int nt_n, nch;
-    if (which == 0) {
-        nch = p.H / 128;
-        src = GlobalRows{p.xr + (size_t)proj * p.nslot_max * p.H, (size_t)p.H, p.xsum + (size_t)proj * p.nslot_max * nch, nch};
-        part = p.part_gu + ((size_t)ks * 2 + proj) * nslot * p.I;
-        part_stride = (size_t)p.I;
-        nt_n = p.I / 16;
-    } else {
-        nch = p.I / 128;
-        src = GlobalRows{p.act, (size_t)p.I, p.actsum, nch};
-        part = p.part_d + (size_t)ks * nslot * p.H;
-        part_stride = (size_t)p.H;
-        nt_n = p.H / 16;
-    }
-    const int kt0 = 8 * (nch * ks / S), kt1 = 8 * (nch * (ks + 1) / S);
-    switch (k2) {
-        case 3: mfma_item_wg_rows<3>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 4: mfma_item_wg_rows<4>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 5: mfma_item_wg_rows<5>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 6: mfma_item_wg_rows<6>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 7: mfma_item_wg_rows<7>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 8: mfma_item_wg_rows<8>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        case 10: mfma_item_wg_rows<10>(trellis, nt_n, cg, kt0, kt1, src, slot_of, rows, part, part_stride, lds); break;
-        default: {
-            // unsupported rate (flagged by the grouping): zero partials, so no output reads stale data
-            const int lane = threadIdx.x & 63;
-            const int wave = threadIdx.x >> 6;
-            for (int r = 0; r < rows; ++r) {
-                float* dst = part + (size_t)slot_of[r] * part_stride + 128 * cg + 32 * wave;
-                if (lane < 32) dst[lane] = 0.0f;
-            }
-        }
-    }
-}
-
-__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(3))) void moe_gate_up_wg_kernel(MoeParams p)
-{
-    __shared__ uint32_t lds[MFW_LDS_WORDS];
-    mfma_stage_wg<0>(p, lds);
-}
-
-__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(3))) void moe_down_wg_kernel(MoeParams p)
-{
-    __shared__ uint32_t lds[MFW_LDS_WORDS];
-    mfma_stage_wg<1>(p, lds);
-}
-
 // The two projection stages as kernels of their own names, so that kernel traces and counter
 // runs tell them apart whatever their grids.
 template <int MBMAX>
@@ -270,16 +170,6 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(M
 {
     __shared__ uint32_t lds[MF_WAVES][MF_LDS_WORDS];
     mfma_stage<MBMAX, 1>(p, lds);
-}
-
-// Calls of more than 16 tokens run the cooperative form of the MFMA stages only when
-// EVAMX_PREFILL_FORM=coop is set in the environment (read at each call): on MI355X it is no faster
-// than the single-wave form at 512 tokens (gate/up level, down 20% slower), and it is kept to
-// reproduce that comparison. Both forms give bit-identical partials.
-bool prefill_coop_form_requested()
-{
-    const char* v = getenv("EVAMX_PREFILL_FORM");
-    return v && strcmp(v, "coop") == 0;
 }
 
 // Side stream of the calling thread on the current device, with its fork and join events, for
@@ -394,11 +284,7 @@ int launch_mfma(const MoeParams& p, int which, hipStream_t stream, hipEvent_t st
     auto k16 = which == 0 ? moe_gate_up_mfma_kernel<1> : moe_down_mfma_kernel<1>;
     auto k64 = which == 0 ? moe_gate_up_mfma_kernel<4> : moe_down_mfma_kernel<4>;
     const dim3 grid = mfma_grid(p, which), block(64 * MF_WAVES);
-    if (p.T > EVAMX_SMALL_TILE_ROWS && prefill_coop_form_requested()) {
-        // cooperative form: one item per workgroup
-        const dim3 wg_grid((unsigned)((items + 7) & ~7L));
-        launch_timed(which == 0 ? moe_gate_up_wg_kernel : moe_down_wg_kernel, wg_grid, block, stream, start, stop, p);
-    } else if (const SideStream* side = p.T > EVAMX_SMALL_TILE_ROWS && p.side_ok ? side_stream(stream) : nullptr) {
+    if (const SideStream* side = p.T > EVAMX_SMALL_TILE_ROWS && p.side_ok ? side_stream(stream) : nullptr) {
         // the tiles of at most 16 rows in the 16-row kernel on the side stream, concurrently with
         // the larger ones in the 64-row kernel on the caller's stream: each fills the other's
         // last round (two kernels of different register budgets cannot share one grid)

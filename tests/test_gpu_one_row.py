@@ -144,39 +144,6 @@ def test_one_row_graph_replays(dev):
         assert rel_err_rows(y_graph.cpu().numpy(), ref) < TOL
 
 
-@pytest.mark.parametrize("K", [2, 3, 4, 5, 2.5])
-def test_one_row_table_decode_variant(dev, K):
-    """The opt-in LDS-table decode of the one-row gate/up launch (EVAMX_GATE_UP_DECODE=table,
-    column groups a multiple of 8) decodes the same fp16 values in the same order: its output
-    equals the default decode's bit for bit, and the oracle within the tolerance."""
-    import os
-    from eva_amd import ops
-    H, I, E, k = 512, 1024, 12, 4
-    rng = np.random.default_rng(45)
-    ex = _experts(rng, H, I, E, K)
-    sh = synth.expert(rng, H, I, K, 1 / np.sqrt(H))
-    de, ds = DeviceExperts(ex, dev), DeviceExperts([sh], dev)
-    x = synth.activations_bf16(rng, 1, H)
-    z = synth.logits_plain(rng, 1, E)
-    ws = ops.MoeWorkspace(dev, rows_max=1, hidden=H, inter=I, topk=k, n_local=E, has_shared=True)
-    sel = torch.empty(1, k, dtype=torch.int64, device=dev)
-    w = torch.empty(1, k, dtype=torch.float32, device=dev)
-    outs = []
-    for mode in (None, "table"):
-        if mode:
-            os.environ["EVAMX_GATE_UP_DECODE"] = mode
-        try:
-            out = torch.empty(1, H, dtype=torch.float32, device=dev)
-            ops.moe_forward(ws, to_dev(x, dev).to(torch.bfloat16), de.table, out, limit=10.0, bits=K,
-                            logits=to_dev(z, dev), sel=sel, weights=w, shared_ptrs=ds.ptrs(0), shared_bits=K)
-            torch.cuda.synchronize()
-        finally:
-            os.environ.pop("EVAMX_GATE_UP_DECODE", None)
-        outs.append(out.cpu().numpy())
-    assert np.array_equal(outs[0], outs[1])
-    ref, _, _, _ = coop.moe_layer(x, z, ex, sh, k, 10.0)
-    assert rel_err_rows(outs[1], ref) < TOL
-
 
 @pytest.mark.parametrize("E,k,score,bias", [(384, 16, "sigmoid", False), (384, 8, "sqrt_softplus", True),
                                             (64, 32, "sigmoid", True)])
