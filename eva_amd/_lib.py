@@ -13,12 +13,13 @@ import torch  # noqa: F401  (loads the HIP runtime the library resolves against)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libevamx.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 EVAMX_OK, EVAMX_EINVAL, EVAMX_ELAUNCH, EVAMX_ENOSPACE = 0, -1, -2, -3
 DTYPE_F16, DTYPE_BF16 = 0, 1
 SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS = 0, 1
 ERR_EXPERT_RANGE, ERR_RATE = 1, 2
+STRICT_MAX_ROWS, STRICT_MAX_SLOTS = 64, 256      # EVAMX_STRICT_MAX_ROWS / EVAMX_STRICT_MAX_SLOTS
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -27,7 +28,8 @@ _f32 = ctypes.c_float
 
 class MoeShape(ctypes.Structure):
     _fields_ = [("rows_max", _i32), ("hidden", _i32), ("inter", _i32), ("topk", _i32),
-                ("n_local", _i32), ("has_shared", _i32), ("ksplit_gu", _i32), ("ksplit_down", _i32)]
+                ("n_local", _i32), ("has_shared", _i32), ("ksplit_gu", _i32), ("ksplit_down", _i32),
+                ("strict_rows", _i32)]                                              # ABI 5
 
 
 class MoeArgs(ctypes.Structure):

@@ -21,14 +21,17 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import ops, verification
 from .pack import PackIndex, load_layers, read_index
 
 
 class ResidentExperts:
     """Experts of ``layers`` of a DS41PK01 pack (default all) resident on ``device``."""
 
-    def __init__(self, pack, device=None, layers=None, topk: int = 8, max_rows: int = 16):
+    def __init__(self, pack, device=None, layers=None, topk: int = 8, max_rows: int = 16, *,
+                 strict_rows: int | None = None):
+        """``strict_rows`` None follows DS41_STRICT_BATCH / DS41_VERIFY_MAX_ROWS (calls of up to the
+        verification bound give every row a one-row call's bits); 0 turns strict mode off."""
         index = pack if isinstance(pack, PackIndex) else read_index(pack)
         self.index = index
         self.device = torch.device("cuda", 0) if device is None else torch.device(device)
@@ -39,6 +42,7 @@ class ResidentExperts:
         self.n_experts = index.n_experts
         self.topk = topk
         self.max_rows = max_rows
+        self.strict_rows = strict_rows
         # [L, 9, N] pointer tables and [L, N] rates (2 x bits) of the resident layers, in layer order
         self.packed = torch.stack([self._layers[l].table for l in self.layer_ids])
         self.k2 = torch.stack([self._layers[l].k2 for l in self.layer_ids])
@@ -52,8 +56,10 @@ class ResidentExperts:
         ws = self._ws.get(key)
         if ws is None or ws.shape.rows_max < rows:
             cap = max(rows, self.max_rows)
+            strict = (verification.moe_strict_rows(cap, topk) if self.strict_rows is None
+                      else min(self.strict_rows, cap))
             ws = ops.MoeWorkspace(self.device, rows_max=cap, hidden=self.hidden, inter=self.inter, topk=topk,
-                                  n_local=self.n_experts, has_shared=has_shared)
+                                  n_local=self.n_experts, has_shared=has_shared, strict_rows=strict)
             self._ws[key] = ws
         return ws
 

@@ -28,12 +28,18 @@ Differences, all on the side of fewer host round trips:
 from __future__ import annotations
 
 import contextlib
+import ctypes
+import dataclasses
+import hashlib
+import json
 import math
+import os
 import threading
 
 import torch
 
 from . import ops
+from . import verification
 
 RATES = (1.5, 2, 2.5, 3, 3.5, 4, 5)
 
@@ -76,10 +82,14 @@ class CoopRunner:
     """Fixed-row decode runner (runtime/ds41/moe_coop.py:15-69). ``run`` returns a borrowed
     fp32 ``[rows, hidden]`` that the next call overwrites."""
 
-    def __init__(self, device, topk: int, hidden: int, inter: int, rows: int = 1, n_local: int | None = None):
+    def __init__(self, device, topk: int, hidden: int, inter: int, rows: int = 1, n_local: int | None = None,
+                 *, strict_rows: int | None = None):
         slots = topk * rows
         if rows < 1 or slots > 256:
             raise ValueError("Cooperative EXL3 supports 1..256 routed slots")
+        # strict batch mode (DS41_STRICT_BATCH, default on; moe_coop.py:17-22): calls of up to the
+        # verification bound compute every row as a one-row call would
+        self.strict_rows = verification.moe_strict_rows(rows, topk) if strict_rows is None else strict_rows
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("CoopRunner needs a GPU device")
@@ -95,7 +105,7 @@ class CoopRunner:
         ws = self._ws.get(n_local)
         if ws is None:
             ws = ops.MoeWorkspace(self.device, rows_max=self.rows, hidden=self.hi, inter=self.inter, topk=self.topk,
-                                  n_local=n_local, has_shared=False)
+                                  n_local=n_local, has_shared=False, strict_rows=self.strict_rows)
             self._ws[n_local] = ws
         return ws
 
@@ -201,7 +211,7 @@ class CoopRunnerCapacity:
     OWNED_OUTPUT = True
 
     def __init__(self, device="cuda", topk=6, hidden=5120, inter=2304, max_rows=None, *, n_local=None,
-                 verbose=False):
+                 verbose=False, strict_rows=None):
         max_rows = self.DEFAULT_MAX_ROWS if max_rows is None else max_rows
         if type(topk) is not int or not 1 <= topk <= 32:
             raise ValueError("topk must be an integer in 1..32")
@@ -221,6 +231,9 @@ class CoopRunnerCapacity:
                 raise RuntimeError("runner construction during capture is unsupported")
         self.topk, self.hidden, self.inter, self.max_rows = topk, hidden, inter, max_rows
         self.n_local = n_local
+        # strict batch mode (DS41_STRICT_BATCH, default on: moe_coop.py:17-22, cache.py:2088-2091):
+        # calls of up to the verification bound give every row the bits of a one-row call
+        self.strict_rows = verification.moe_strict_rows(max_rows, topk) if strict_rows is None else strict_rows
         self.verbose = verbose
         self._own = _Ownership(self.device)
         self._table_valid = False
@@ -238,7 +251,7 @@ class CoopRunnerCapacity:
         ws = self._ws.get(n_local)
         if ws is None:
             ws = ops.MoeWorkspace(self.device, rows_max=self.max_rows, hidden=self.hidden, inter=self.inter,
-                                  topk=self.topk, n_local=n_local, has_shared=False)
+                                  topk=self.topk, n_local=n_local, has_shared=False, strict_rows=self.strict_rows)
             self._ws[n_local] = ws
         return ws
 
@@ -342,3 +355,84 @@ class CoopRunner2048(CoopRunnerCapacity):
 class CoopRunner3072(CoopRunnerCapacity):
     """runtime/ds41/moe_coop3072.py:261 (default capacity 512 rows)."""
     DEFAULT_MAX_ROWS = 512
+
+
+@dataclasses.dataclass(frozen=True)
+class WorkspaceLayout:
+    """Device memory a capacity runner owns (moe_coop3072.py:120-152, read by its production owner
+    as ``WorkspaceLayout().scratch_bytes``, native3072_runtime.py:134,146): the libevamx MoE
+    workspace (``evamx_moe_workspace_bytes``) plus the runner's own output rows, fp16 routing
+    weights, run table and prepare_routes workspace. Defaults are the reference's checkpoint
+    shape (512 rows, H5120, I2304, top-6, up to 384 local experts); every field is a parameter
+    here, and ``strict_rows`` None follows DS41_STRICT_BATCH / DS41_VERIFY_MAX_ROWS as the
+    runners do."""
+
+    max_rows: int = 512
+    hidden: int = 5120
+    inter: int = 2304
+    topk: int = 6
+    n_local: int = 384
+    has_shared: bool = False
+    strict_rows: int | None = None
+
+    def __post_init__(self):
+        for name in ("max_rows", "hidden", "inter", "topk", "n_local"):
+            if type(getattr(self, name)) is not int or getattr(self, name) < 1:
+                raise ValueError(f"{name} must be a positive integer")
+        if self.hidden % 128 or self.inter % 128:
+            raise ValueError("hidden and inter must be multiples of 128")
+
+    @property
+    def slots(self) -> int:
+        return self.max_rows * self.topk
+
+    @property
+    def run_table_ints(self) -> int:
+        """Length of the run table (moe_coop3072.py:97-106): 2 + 2 * slots + 1."""
+        return 2 + 2 * self.slots + 1
+
+    @property
+    def moe_workspace_bytes(self) -> int:
+        strict = (verification.moe_strict_rows(self.max_rows, self.topk) if self.strict_rows is None
+                  else self.strict_rows)
+        shape = ops.MoeShape(self.max_rows, self.hidden, self.inter, self.topk, self.n_local, int(self.has_shared),
+                             0, 0, strict)
+        n = ops.lib().evamx_moe_workspace_bytes(ctypes.byref(shape))
+        if n == 0:
+            raise ValueError("invalid MoE shape: " + ops.lib().evamx_last_error().decode())
+        return n
+
+    @property
+    def scratch_bytes(self) -> int:
+        return (self.moe_workspace_bytes + self.max_rows * self.hidden * 4 + self.slots * 2
+                + self.run_table_ints * 4 + ops.prepare_routes_workspace_bytes(self.max_rows, self.topk))
+
+
+def source_metadata() -> dict:
+    """Build identity of the library behind these runners (moe_coop3072.py's source_metadata
+    reports the reference extension's): hashes of the HIP sources and the C header (sorted by
+    relative POSIX path), of the compile recipe and of the built library, the ABI version, and
+    the arithmetic geometry a caller pins a target to."""
+    from . import _lib, build
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    files = sorted([os.path.join(build.CSRC, f) for f in os.listdir(build.CSRC)
+                    if f.endswith((".hip", ".hpp"))] + [os.path.join(root, "include", "evamx.h")],
+                   key=lambda f: os.path.relpath(f, root).replace(os.sep, "/"))
+    h = hashlib.sha256()
+    for f in files:
+        h.update(os.path.relpath(f, root).replace(os.sep, "/").encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    recipe = {"source_sha256": h.hexdigest(), "hipcc_flags": list(build.FLAGS), "arch": build.ARCH}
+    build_sha = hashlib.sha256(json.dumps(recipe, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
+    lib_sha = None
+    if os.path.exists(_lib.LIB_PATH):
+        with open(_lib.LIB_PATH, "rb") as fh:
+            lib_sha = hashlib.sha256(fh.read()).hexdigest()
+    return {"source_sha256": recipe["source_sha256"], "build_sha256": build_sha, "library_sha256": lib_sha,
+            "source_files": len(files), "hipcc_flags": list(build.FLAGS), "arch": build.ARCH,
+            "abi_version": _lib.ABI_VERSION, "codebook": "MUL1", "K": list(RATES),
+            "strict_batch": verification.strict_batch(), "verification_max_rows": verification.verification_max_rows(),
+            "strict_max_rows": verification.STRICT_MOE_MAX_ROWS, "strict_max_slots": verification.STRICT_MOE_MAX_SLOTS,
+            "max_topk": 32, "max_local_experts": 512, "graph_capture_supported": True,
+            "output_ownership": "owned clone (CoopRunner2048/3072), borrowed rows (CoopRunner, CoopRunner512)"}

@@ -43,6 +43,7 @@ struct MoeLayout {
     size_t flags, meta, local, order, runs, chunks, unit_chunk, tiles, slot_mult, rw16, urec, srec, gate_val, logits, xr,
         xsum, act, actsum, part_gu, part_d, total;
     int slots_max, nslot_max, max_chunks, ks_gu, ks_d, ks_gu_max, ks_d_max, cap_rows_gu, cap_rows_d;
+    int strict_ks_gu, strict_ks_d;
 };
 
 // Rows of GEMV partials a workspace holds when the k-split is chosen on the device: enough
@@ -83,7 +84,37 @@ static bool shape_ok(const evamx_moe_shape* s)
         return false;
     }
     if ((long)s->rows_max * s->topk > 65536) { set_error("evamx: rows_max*topk above 65536"); return false; }
+    if (s->strict_rows < 0 || s->strict_rows > EVAMX_STRICT_MAX_ROWS || s->strict_rows * s->topk > EVAMX_STRICT_MAX_SLOTS) {
+        set_error("evamx: strict_rows %d outside 0..%d (at most %d slots)", s->strict_rows, EVAMX_STRICT_MAX_ROWS,
+                  EVAMX_STRICT_MAX_SLOTS);
+        return false;
+    }
     return true;
+}
+
+// Rows of a call that the decode path serves with this shape: up to EVAMX_GEMV_MAX_ROWS, and up
+// to strict_rows in strict mode.
+static int decode_rows(const evamx_moe_shape* s)
+{
+    const int r = s->strict_rows > EVAMX_GEMV_MAX_ROWS ? s->strict_rows : EVAMX_GEMV_MAX_ROWS;
+    return s->rows_max < r ? s->rows_max : r;
+}
+
+// K-splits of strict mode: the ones a one-row call picks on its own (split_waves / moe_ksplit at
+// T = 1 on the decode path: the one-row unit count, half a resident round of waves), or the
+// requested ones; both depend on the shape and the device only, never on the call's rows.
+static void strict_splits(const evamx_moe_shape* s, int kgu_max, int kd_max, int& gu, int& d)
+{
+    const int units1 = s->topk + (s->has_shared ? 1 : 0);
+    const int waves = gemv_waves() / 2;
+    auto pick = [&](int req, int items, int kmax) {
+        if (req > 0) return req < kmax ? req : kmax;
+        int b = waves / items;
+        if (b > kmax) b = kmax;
+        return b < 1 ? 1 : b;
+    };
+    gu = pick(s->ksplit_gu, units1 * 2 * (s->inter / 128), kgu_max);
+    d = pick(s->ksplit_down, units1 * (s->hidden / 128), kd_max);
 }
 
 static MoeLayout moe_layout(const evamx_moe_shape* s)
@@ -100,6 +131,16 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     const int auto_rows = L.nslot_max > EVAMX_AUTO_PART_ROWS ? L.nslot_max : EVAMX_AUTO_PART_ROWS;
     L.cap_rows_gu = L.ks_gu ? L.ks_gu * L.nslot_max : auto_rows;
     L.cap_rows_d = L.ks_d ? L.ks_d * L.nslot_max : auto_rows;
+    const int dr = decode_rows(s);
+    L.strict_ks_gu = L.strict_ks_d = 0;
+    if (s->strict_rows > 0) {
+        // strict calls keep the one-row splits at every row count up to strict_rows
+        strict_splits(s, L.ks_gu_max, L.ks_d_max, L.strict_ks_gu, L.strict_ks_d);
+        const int sr = s->rows_max < s->strict_rows ? s->rows_max : s->strict_rows;
+        const int nslot_s = sr * s->topk + (s->has_shared ? sr : 0);
+        if (L.cap_rows_gu < L.strict_ks_gu * nslot_s) L.cap_rows_gu = L.strict_ks_gu * nslot_s;
+        if (L.cap_rows_d < L.strict_ks_d * nslot_s) L.cap_rows_d = L.strict_ks_d * nslot_s;
+    }
     size_t o = 0;
     L.flags = o;   o = al256(o + 64 * 4);     // first: evamx_moe_forward_static zeroes offset 0 of its scratch
     L.meta = o;    o = al256(o + 64 * 4);
@@ -111,12 +152,10 @@ static MoeLayout moe_layout(const evamx_moe_shape* s)
     L.tiles = o;   o = al256(o + (size_t)L.max_chunks * 4);
     L.slot_mult = o; o = al256(o + (size_t)L.nslot_max * 4);
     L.rw16 = o;    o = al256(o + (size_t)L.slots_max * 2);
-    {
-        // decode-path records: calls of at most EVAMX_GEMV_MAX_ROWS rows
-        const int dr = s->rows_max < EVAMX_GEMV_MAX_ROWS ? s->rows_max : EVAMX_GEMV_MAX_ROWS;
-        L.urec = o; o = al256(o + (size_t)(dr * s->topk + 1) * sizeof(UnitRec));
-        L.srec = o; o = al256(o + (size_t)dr * (s->topk + 1) * sizeof(SlotRec));
-    }
+    // decode-path records of calls of at most dr rows: a unit per routed slot at most (a chunk's
+    // weight never exceeds its rows) and the shared expert's chunks of EVAMX_CHUNK rows
+    L.urec = o; o = al256(o + (size_t)moe_units_max(dr, s->topk, s->has_shared) * sizeof(UnitRec));
+    L.srec = o; o = al256(o + (size_t)dr * (s->topk + 1) * sizeof(SlotRec));
     L.gate_val = o; o = al256(o + (size_t)s->rows_max * 4);
     L.logits = o;  o = al256(o + (size_t)s->rows_max * EVAMX_MAX_EXPERTS * 4);
     L.xr = o;      o = al256(o + (size_t)2 * L.nslot_max * s->hidden * 2);
@@ -164,7 +203,7 @@ using namespace evamx;
 
 extern "C" const char* evamx_last_error(void) { return g_err; }
 
-extern "C" int evamx_abi_version(void) { return 4; }
+extern "C" int evamx_abi_version(void) { return 5; }
 
 extern "C" int evamx_exl3_dequant(const void* trellis, int in_features, int out_features, float bits, void* w_fp16,
                                   evamx_stream_t stream)
@@ -455,6 +494,8 @@ int evamx::moe_forward_ws(const evamx_moe_args* a, void* workspace, size_t works
     p.ks_gu = L.ks_gu; p.ks_d = L.ks_d;
     p.ks_gu_max = L.ks_gu_max; p.ks_d_max = L.ks_d_max;
     p.cap_rows_gu = L.cap_rows_gu; p.cap_rows_d = L.cap_rows_d;
+    p.strict_rows = s->strict_rows;
+    p.strict_ks_gu = L.strict_ks_gu; p.strict_ks_d = L.strict_ks_d;
     p.gemv_waves = gemv_waves();
     p.side_ok = side_stream_ok ? 1 : 0;
     p.out = a->out; p.out_stride = a->out_stride;

@@ -57,6 +57,14 @@ __device__ __forceinline__ void had128_pair(float& v0, float& v1, int lane)
     v1 *= R_SCALE;
 }
 
+// The codebook's affine map applied to a column's sums: sum_k x_k w_k = 0x1eee * sum_k x_k h_k +
+// 0xc931 * sum_k x_k, with one explicit fused multiply-add, so that no kernel's row count can change
+// how the compiler contracts it (a row's bits must not depend on its call's row count).
+__device__ __forceinline__ float mul1_affine(float acc, float xs)
+{
+    return __builtin_fmaf(MUL1_K_INV, acc, MUL1_K_BIAS * xs);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Streaming loads.
 
@@ -397,8 +405,8 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
                 float xs = 0.0f;                                                                \
                 for (int c = c0; c < c1; ++c) xs += sp[c];                                      \
                 float* dst = part + (size_t)row * part_stride;                                  \
-                dst[col0] = MUL1_K_INV * acc[m][0] + MUL1_K_BIAS * xs;                          \
-                dst[col1] = MUL1_K_INV * acc[m][1] + MUL1_K_BIAS * xs;                          \
+                dst[col0] = mul1_affine(acc[m][0], xs);                                         \
+                dst[col1] = mul1_affine(acc[m][1], xs);                                         \
             }                                                                                   \
         }                                                                                       \
     }

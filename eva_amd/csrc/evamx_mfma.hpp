@@ -176,7 +176,7 @@ __device__ __forceinline__ void mfma_item(const uint32_t* __restrict__ trellis, 
             if (row < rows) {
                 float* dst = part + (size_t)slot_of[row] * part_stride + 128 * cg + m16;
 #pragma unroll
-                for (int nb = 0; nb < 8; ++nb) dst[16 * nb] = MUL1_K_INV * acc[mb][nb][r] + MUL1_K_BIAS * xs[mb][r];
+                for (int nb = 0; nb < 8; ++nb) dst[16 * nb] = mul1_affine(acc[mb][nb][r], xs[mb][r]);
             }
         }
     }

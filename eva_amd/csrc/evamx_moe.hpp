@@ -27,6 +27,10 @@ enum { PREP_GROUP = 1, PREP_MOE = 2 };
 
 // Calls of at most this many rows take the decode path (decode GEMVs, work resolved from records).
 constexpr int EVAMX_GEMV_MAX_ROWS = EVAMX_MFMA_MIN_ROWS - 1;
+// Calls of at most EVAMX_SMALL_ROWS rows and EVAMX_SMALL_SLOTS slots on the MFMA path take the
+// one-launch small prepare and the per-token combine.
+constexpr int EVAMX_SMALL_SLOTS = 512;
+constexpr int EVAMX_SMALL_ROWS = 16;
 
 // Records of the decode path, written by its prepare so that every later kernel resolves its
 // work with one load instead of a chain of dependent ones (unit -> chunk -> pointer table ->
@@ -122,7 +126,10 @@ struct MoeParams {
                                // allocation-free entry point)
     UnitRec* urec;             // decode path: [units_max] work-unit records
     SlotRec* srec;             // decode path: [T * topk + T] slot records (routed slots, shared rows)
-    int units_max;             // decode path: work units the launch grids cover (T * topk + has_shared)
+    int units_max;             // decode path: work units the launch grids cover (moe_units_max)
+    int strict_rows;           // strict batch mode: calls of up to this many rows (0: off) ...
+    int strict_ks_gu, strict_ks_d;   // ... run the decode path with these (one-row) k-splits
+    int strict;                // this call is strict: every chunk weighs 1 and takes the same splits
     // output
     float* out;                // or null
     int out_stride;
@@ -151,6 +158,17 @@ __host__ __device__ __forceinline__ int moe_nslot(const MoeParams& p) { return p
 // of weight 1; a chunk of weight m gets m times the k-splits of a one-row chunk.
 constexpr int EVAMX_MAX_MULT = 3;
 __host__ __device__ __forceinline__ int chunk_mult(int rows) { return rows <= 3 ? 1 : rows <= 6 ? 2 : 3; }
+// The weight of a decode-path chunk in this call: 1 in strict mode (every chunk takes the strict
+// splits, whatever its rows), else chunk_mult.
+__host__ __device__ __forceinline__ int unit_mult(const MoeParams& p, int rows) { return p.strict ? 1 : chunk_mult(rows); }
+
+// Work units of a decode-path call of T rows: at most one per routed slot (a chunk's weight never
+// exceeds its rows) and one per EVAMX_CHUNK rows of the shared expert (its chunks weigh 1:
+// strict mode, or at most 2 rows).
+__host__ __device__ __forceinline__ int moe_units_max(int T, int topk, int has_shared)
+{
+    return T * topk + (has_shared ? (T + EVAMX_CHUNK - 1) / EVAMX_CHUNK : 0);
+}
 
 // K-split choice of a GEMV: `base` splits per work unit, as many as fill the resident grid once
 // (or the requested count), a chunk of weight m gets min(base * m, cap) splits (base when the
@@ -211,6 +229,22 @@ __host__ __device__ __forceinline__ KSplit ks_down(const MoeParams& p, int units
 __host__ __device__ __forceinline__ int chunk_rows_of(const MoeParams& p) { return p.chunk_rows > 0 ? p.chunk_rows : EVAMX_CHUNK; }
 
 int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);
+// Stage launches of moe_launch, one translation unit each (moe_prepare.hip, moe_gate_up*.hip,
+// moe_down.hip, moe_epilogue.hip). start/stop: events that take the first kernel's start and the
+// last kernel's end timestamps (nullptr: none).
+void launch_router_front(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_prepare(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+// Decode-path gate/up: tmax 1 the one-row launch that routes inside, 2 chunks in passes of up to
+// 2 rows, 8 up to 8 rows per pass (falls back to 2-row passes when the column groups are not a
+// multiple of the workgroup's 4 waves).
+void launch_gate_up_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_gate_up_decode8(const MoeParams& p, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_gate_up_decode2(const MoeParams& p, bool group, dim3 grid, hipStream_t stream, hipEvent_t start,
+                            hipEvent_t stop);
+void launch_down_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_act_class(const MoeParams& p, int cls, hipStream_t stream);
+void launch_combine(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 // Kernel launch that, given events, records the kernel's own start and end timestamps in them
 // (hipExtLaunchKernel), as a profiler's kernel trace reports them; plain launch otherwise.
 template <typename... KArgs, typename... Args>

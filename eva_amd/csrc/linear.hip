@@ -120,8 +120,8 @@ __device__ __forceinline__ void lin_rows(const LinParams& p, int r0, int tm, int
     for (int m = 0; m < TM; ++m) {
         if (m < tm) {
             float* dst = p.part + ((size_t)ks * p.rows + r0 + m) * p.out;
-            dst[col0] = MUL1_K_INV * acc[m][0] + MUL1_K_BIAS * xs[m];
-            dst[col1] = MUL1_K_INV * acc[m][1] + MUL1_K_BIAS * xs[m];
+            dst[col0] = mul1_affine(acc[m][0], xs[m]);
+            dst[col1] = mul1_affine(acc[m][1], xs[m]);
         }
     }
 }
@@ -258,7 +258,7 @@ __device__ __forceinline__ void lin_mfma_tile(const LinParams& p, int r0, int ro
 #pragma unroll
             for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) pv[mb][nb][r] = MUL1_K_INV * acc[mb][nb][r] + MUL1_K_BIAS * xs[mb][r];
+                for (int r = 0; r < 4; ++r) pv[mb][nb][r] = mul1_affine(acc[mb][nb][r], xs[mb][r]);
     }
     for (int w = 0; w < p.ks; ++w) {
         __syncthreads();

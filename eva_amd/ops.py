@@ -152,8 +152,11 @@ class MoeWorkspace:
     """Device workspace of the MoE forward for one shape (owned by one runner)."""
 
     def __init__(self, device, rows_max: int, hidden: int, inter: int, topk: int, n_local: int,
-                 has_shared: bool, ksplit_gu: int = 0, ksplit_down: int = 0):
-        self.shape = MoeShape(rows_max, hidden, inter, topk, n_local, int(bool(has_shared)), ksplit_gu, ksplit_down)
+                 has_shared: bool, ksplit_gu: int = 0, ksplit_down: int = 0, strict_rows: int = 0):
+        """``strict_rows`` > 0: calls of up to that many rows give every row the bits it gets in a
+        one-row call (strict batch mode, the reference's DS41_STRICT_BATCH); 0: automatic geometry."""
+        self.shape = MoeShape(rows_max, hidden, inter, topk, n_local, int(bool(has_shared)), ksplit_gu, ksplit_down,
+                              strict_rows)
         nbytes = lib().evamx_moe_workspace_bytes(ctypes.byref(self.shape))
         if nbytes == 0:
             raise ValueError("invalid MoE shape: " + lib().evamx_last_error().decode())

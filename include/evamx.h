@@ -111,7 +111,19 @@ typedef struct evamx_moe_shape {
     int32_t ksplit_gu;    /* k-splits of the gate/up GEMV (0: chosen per call on the device
                              from the number of expert chunks, to fill the GPU once) */
     int32_t ksplit_down;  /* k-splits of the down GEMV (0: likewise) */
+    /* ABI 5. Strict batch mode, the reference's DS41_STRICT_BATCH (moe_coop.py:17-22, which pins
+     * EXL3_MOE_COOP_WIDE=0 / EXL3_MOE_COOP_KSPLIT=1 so that "target and verification arithmetic"
+     * stay identical; cache.py:2088-2091), bounded by its verification row limit
+     * (verification.py:15-30). 0: every call picks its product path and k-splits from its row
+     * count (fastest). 1..EVAMX_STRICT_MAX_ROWS (with strict_rows * topk <= EVAMX_STRICT_MAX_SLOTS):
+     * calls of 1..strict_rows rows run every row through the arithmetic of a one-row call (the
+     * decode GEMV with the k-splits a one-row call picks, or ksplit_gu/ksplit_down when given), so
+     * each row's output is bit-identical whatever the call's row count in that range. Calls of
+     * more rows keep the automatic geometry. */
+    int32_t strict_rows;
 } evamx_moe_shape;
+
+enum { EVAMX_STRICT_MAX_ROWS = 64, EVAMX_STRICT_MAX_SLOTS = 256 };
 
 typedef struct evamx_moe_args {
     evamx_moe_shape shape;

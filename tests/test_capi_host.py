@@ -53,7 +53,8 @@ def test_struct_layout_matches_header(tmp_path):
 
 
 def _shape(**kw):
-    d = dict(rows_max=16, hidden=7168, inter=2048, topk=8, n_local=256, has_shared=1, ksplit_gu=0, ksplit_down=0)
+    d = dict(rows_max=16, hidden=7168, inter=2048, topk=8, n_local=256, has_shared=1, ksplit_gu=0, ksplit_down=0,
+             strict_rows=0)
     d.update(kw)
     return _lib.MoeShape(*[d[f] for f, _ in _lib.MoeShape._fields_])
 
@@ -66,10 +67,19 @@ def test_workspace_bytes():
     # DSv3 T=16 scratch is small next to the 2.27 GB of weights the step reads
     assert sizes[2] < 64 << 20
     for bad in (dict(hidden=7100), dict(inter=0), dict(topk=0), dict(topk=33), dict(n_local=513),
-                dict(rows_max=0), dict(ksplit_gu=65), dict(rows_max=65536, topk=8)):
+                dict(rows_max=0), dict(ksplit_gu=65), dict(rows_max=65536, topk=8), dict(strict_rows=-1),
+                dict(strict_rows=65, topk=1), dict(strict_rows=33, topk=8)):
         assert L.evamx_moe_workspace_bytes(ctypes.byref(_shape(**bad))) == 0, bad
         assert L.evamx_last_error()
     assert L.evamx_prepare_routes_workspace_bytes(0, 8) == 0
+    # strict mode: room for the decode path's records and one-row splits at every row count up to
+    # strict_rows; DSv3 strict verification batches of 16 rows stay far below the weights they read
+    for r in (1, 2, 16, 32):
+        plain = L.evamx_moe_workspace_bytes(ctypes.byref(_shape(rows_max=r)))
+        strict = L.evamx_moe_workspace_bytes(ctypes.byref(_shape(rows_max=r, strict_rows=min(r, 32))))
+        assert strict >= plain > 0
+    assert L.evamx_moe_workspace_bytes(ctypes.byref(_shape(rows_max=16, strict_rows=16))) < 64 << 20
+    assert L.evamx_moe_workspace_bytes(ctypes.byref(_shape(rows_max=512, strict_rows=8))) > 0
     assert L.evamx_exl3_linear_workspace_bytes(1, 2048, 7168) > 2048 * 2
 
 

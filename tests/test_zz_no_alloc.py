@@ -35,7 +35,7 @@ def _run(ops, dev, case, x, logits, static, rows_max=ROWS_MAX):
               shared_bits=4)
     xt = to_dev(x, dev).to(torch.bfloat16)
     if static:
-        ops.moe_forward_static(ops.MoeShape(rows_max, H, I, TOPK, E, 1, 0, 0), xt, de.table, out, **kw)
+        ops.moe_forward_static(ops.MoeShape(rows_max, H, I, TOPK, E, 1, 0, 0, 0), xt, de.table, out, **kw)
     else:
         ws = ops.MoeWorkspace(dev, rows_max=rows_max, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True)
         ws.buffer.fill_(0x7f)
@@ -86,11 +86,11 @@ def test_static_refusals(dev, case):
     from eva_amd import _lib, ops
     L = _lib.lib()
     a = _lib.MoeArgs()
-    a.shape = _lib.MoeShape(4096, 7168, 2048, 8, 256, 1, 0, 0)     # a prefill-size workspace: too big
+    a.shape = _lib.MoeShape(4096, 7168, 2048, 8, 256, 1, 0, 0, 0)     # a prefill-size workspace: too big
     a.rows = 1
     assert L.evamx_moe_forward_static(ctypes.byref(a), None) == _lib.EVAMX_ENOSPACE
     assert b"fixed scratch" in L.evamx_last_error()
-    a.shape = _lib.MoeShape(1, H, I, TOPK, E, 0, 0, 0)
+    a.shape = _lib.MoeShape(1, H, I, TOPK, E, 0, 0, 0, 0)
     a.workspace = 1 << 20
     a.workspace_bytes = 1 << 20
     assert L.evamx_moe_forward_static(ctypes.byref(a), None) == _lib.EVAMX_EINVAL
