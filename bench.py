@@ -23,6 +23,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import platform
 import subprocess
@@ -163,46 +164,69 @@ def cpu_info(torch):
             "mkl": bool(torch.backends.mkl.is_available()), "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
 
 
-def cpu_baseline(torch, layers, l, x_dev, logits_dev, tokens, limit, what):
+def cpu_baseline(torch, layers, ls, x_dev, logits_list, tokens, limit, what, runs=5, warmups=2, scale=1):
     """The PyTorch-CPU restatement (oracle/torch_cpu.py) on the host cores, on the GPU step's own
     inputs: the first ``tokens`` rows of the step's activations (cast to fp16 as Block.experts
-    does) and logits, routed on the CPU (sigmoid top-8), through the experts of layer ``l``
-    copied from HBM (the routed experts those tokens pick and the shared expert). 2 warm-ups,
-    then the median of 5 runs; GB/s over the same algorithmic bytes as the GPU line."""
+    does) and, for each layer of ``ls`` in turn, its logits, routed on the CPU (sigmoid top-8),
+    through the experts of that layer copied from HBM (the routed experts those tokens pick and
+    the shared expert); with several layers each layer's output is added to the stream that
+    feeds the next. ``warmups`` untimed runs (0: one projection decode warms the allocator and
+    the thread pool instead), then the median of ``runs`` runs; GB/s over the same algorithmic
+    bytes as the GPU line. ``scale``: the number of such samples in the GPU step (the seconds
+    per step estimate is scale times the sample's)."""
     from oracle import torch_cpu
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    x = x_dev[:tokens].float().cpu().half().float()
-    z = logits_dev[:tokens].float().cpu()
-    idx, _ = torch_cpu.route_sigmoid(z, TOPK)
-    used = sorted(set(idx.reshape(-1).tolist()))
-    experts = {e: layers.expert_parts(torch, l, e) for e in used}
-    shared = layers.expert_parts(torch, l, -1)
-    decs = {}
-    for e in used + [-1]:
-        rate = layers.rates[l][e if e >= 0 else layers.n - 1]
-        decs.setdefault(rate, torch_cpu.Decoder(rate))
-    dec = {e: decs[layers.rates[l][e if e >= 0 else layers.n - 1]] for e in used + [-1]}
+    x0 = x_dev[:tokens].float().cpu().half().float()
+    plans = []
+    nbytes = 0
+    for l, z_dev in zip(ls, logits_list):
+        z = z_dev[:tokens].float().cpu()
+        idx, _ = torch_cpu.route_sigmoid(z, TOPK)
+        used = sorted(set(idx.reshape(-1).tolist()))
+        experts = {e: layers.expert_parts(torch, l, e) for e in used}
+        shared = layers.expert_parts(torch, l, -1)
+        decs = {}
+        for e in used + [-1]:
+            rate = layers.rates[l][e if e >= 0 else layers.n - 1]
+            decs.setdefault(rate, torch_cpu.Decoder(rate))
+        dec = {e: decs[layers.rates[l][e if e >= 0 else layers.n - 1]] for e in used + [-1]}
+        plans.append((z, experts, shared, dec, len(used)))
+        nbytes += layers.step_bytes(l, used) + tokens * (H * 2 + E * 4 + H * 4)
 
     def run():
-        i, w = torch_cpu.route_sigmoid(z, TOPK)
-        return torch_cpu.moe_layer(x, i, w, experts, shared, dec, limit)
+        h = x0
+        for z, experts, shared, dec, _ in plans:
+            i, w = torch_cpu.route_sigmoid(z, TOPK)
+            y = torch_cpu.moe_layer(h, i, w, experts, shared, dec, limit)
+            h = (h + y).half().float() if len(plans) > 1 else y
+        return h
 
-    for _ in range(2):
-        run()
+    if warmups:
+        for _ in range(warmups):
+            run()
+    else:
+        z, experts, shared, dec, _ = plans[0]
+        tr, suh, svh = shared[0]
+        dec[-1].dequant(tr)
     times = []
-    for _ in range(5):
+    for _ in range(runs):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    t = sorted(times)[2]
-    nbytes = layers.step_bytes(l, used) + tokens * (H * 2 + E * 4 + H * 4)
+    t = sorted(times)[len(times) // 2]
+    counts = " + ".join(f"{p[4]}" for p in plans)
+    layer_txt = f"layer {ls[0]}" if len(ls) == 1 else f"layers {', '.join(str(l) for l in ls)}"
+    runs_txt = (f"median of {runs} runs after {warmups} warm-ups" if warmups
+                else f"{'median of ' + str(runs) + ' runs' if runs > 1 else 'one run'} after a warm-up decode")
     res = {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-           "sample": f"{what}: {tokens} token(s), {len(used)} routed experts + the shared expert of layer {l} "
-                     f"({nbytes / 1e6:.1f} MB), routing included; median of 5 runs after 2 warm-ups "
-                     f"({t:.2f} s per run)",
+           "sample": f"{what}: {tokens} token(s), {counts} routed experts + the shared expert of {layer_txt} "
+                     f"({nbytes / 1e6:.1f} MB), routing included; {runs_txt} ({t:.2f} s per run)",
            "seconds_per_sample": round(t, 3), "runs_s": [round(v, 3) for v in times]}
+    if scale != 1:
+        res["samples_per_step"] = scale
+        res["seconds_per_step_estimate"] = round(t * scale, 2)
     res.update(cpu_info(torch))
     return res
 
@@ -414,6 +438,9 @@ def parse_args():
     ap.add_argument("--routing", choices=("plain", "skewed"), default=None,
                     help="N(0,1) logits, or config 3's per-token bias (default: plain at 1 token, skewed above)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", choices=("strict", "fast"), default="strict",
+                    help="strict (default, as the reference's DS41_STRICT_BATCH): calls of up to 64 tokens give "
+                         "every token a one-token call's bits; fast: the geometry is chosen per call size")
     ap.add_argument("--also-tokens", type=int, default=16,
                     help="with the default 1-token layer, also measure this many tokens (configs[2]) and report "
                          "it under \"also\" in the same line (0: off)")
@@ -469,18 +496,32 @@ def main():
     else:
         result = run_layer(torch, args)
         if args.workload == "layer" and args.tokens == 1 and args.also_tokens > 0:
-            # the metric covers 1 and 16 tokens: the second point rides along in the same line
+            # the metric covers 1 and 16 tokens: the 16-token point rides along in the same line
+            # (same mode, with its own CPU baseline), and both points in the other mode beside them
             import copy
-            import gc
 
-            gc.collect()
-            torch.cuda.empty_cache()
-            sub = copy.copy(args)
-            sub.tokens, sub.routing, sub.no_cpu_baseline = args.also_tokens, None, True
-            r2 = run_layer(torch, sub)
-            result["also"] = {k: r2[k] for k in ("us_per_layer", "value", "unit", "step_bytes", "frac_hbm_step",
-                                                 "kernel_us", "roofline")}
+            other = "fast" if args.mode == "strict" else "strict"
+            keys = ("us_per_layer", "value", "unit", "step_bytes", "frac_hbm_step", "kernel_us", "roofline")
+            runs = {}
+            for mode, T in ((args.mode, args.also_tokens), (other, 1), (other, args.also_tokens)):
+                sub = copy.copy(args)
+                sub.tokens, sub.routing, sub.mode = T, None, mode
+                sub.no_cpu_baseline = args.no_cpu_baseline or mode != args.mode
+                runs[mode, T] = run_layer(torch, sub)
+            r2 = runs[args.mode, args.also_tokens]
+            result["also"] = {k: r2[k] for k in keys + (("cpu_baseline",) if "cpu_baseline" in r2 else ())}
             result["also"]["config"] = r2["config"]["workload"]
+            result["also"]["mode"] = r2["config"]["mode"]
+            result["modes"] = {
+                "headline": args.mode,
+                "note": "strict: calls of up to strict_rows tokens give every token the bits of a one-token "
+                        "call (the reference's default DS41_STRICT_BATCH); at 1 token both modes run the same "
+                        "kernels with the same splits",
+                args.mode: {"us_per_layer_1": result["us_per_layer"], f"us_per_layer_{args.also_tokens}": r2["us_per_layer"]},
+                other: {"us_per_layer_1": runs[other, 1]["us_per_layer"],
+                        f"us_per_layer_{args.also_tokens}": runs[other, args.also_tokens]["us_per_layer"],
+                        f"kernel_us_{args.also_tokens}": runs[other, args.also_tokens]["kernel_us"]},
+            }
     print(json.dumps(result), flush=True)
 
 
@@ -529,6 +570,25 @@ def timed_replays(torch, stream, replay, n, warm):
     return [evs[i].elapsed_time(evs[i + 1]) for i in range(n)], evs[0].elapsed_time(evs[n])
 
 
+def strict_rows_for(mode, T):
+    """strict_rows of the benchmark's workspace: the call's own rows in strict mode (within the
+    strict bound of 64 rows and 256 slots), else 0."""
+    return T if mode == "strict" and T <= 64 and T * TOPK <= 256 else 0
+
+
+_LAYERS = {}
+
+
+def resident_layers(torch, dev, n_layers, bits, **kw):
+    """DeviceLayers of a uniform rate, kept across the runs of one bench process (the extra
+    lines reuse the headline line's resident weights instead of allocating them again)."""
+    key = (n_layers, bits, tuple(sorted(kw.items())))
+    if key not in _LAYERS:
+        _LAYERS.clear()
+        _LAYERS[key] = DeviceLayers(torch, dev, n_layers, bits, **kw)
+    return _LAYERS[key]
+
+
 def median(v):
     v = sorted(v)
     n = len(v)
@@ -559,15 +619,22 @@ def run_layer(torch, args):
                     for _ in range(args.layers)]
         layers = DeviceLayers(torch, dev, args.layers, lambda l, e: rate_tab[l][e], shared_bits=4.0)
     else:
-        layers = DeviceLayers(torch, dev, args.layers, args.bits)
+        layers = resident_layers(torch, dev, args.layers, args.bits)
     g = torch.Generator(device=dev)
     g.manual_seed(99)
-    G = 1 if prefill else args.graph_steps
-    n_draws = max(G, args.layers) * 2
+    # The step sequence cycles C = --graph-steps (layer, routing draw) pairs (one for prefill).
+    # Exactly --steps steps are timed: graph replays of G steps, G the largest divisor of both,
+    # the C/G graphs of the cycle replayed in turn, so the timed draws do not depend on --steps.
+    C = 1 if prefill else args.graph_steps
+    G = math.gcd(max(1, args.steps), C)
+    reps = max(1, args.steps) // G
+    n_graphs = C // G
+    n_draws = max(C, args.layers) * 2
     logits = make_logits(torch, g, dev, n_draws, T, args.routing)
     x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    strict_rows = strict_rows_for(args.mode, T)
     ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
-                          ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down)
+                          ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down, strict_rows=strict_rows)
     sel = torch.empty(T, TOPK, dtype=torch.int64, device=dev)
     wts = torch.empty(T, TOPK, dtype=torch.float32, device=dev)
     out = torch.empty(T, H, dtype=torch.float32, device=dev)
@@ -592,30 +659,36 @@ def run_layer(torch, args):
     act_bytes = T * H * 2 + T * E * 4 + T * H * 4
 
     stream = torch.cuda.Stream(device=dev)
-    graph = None
+    graphs = []
     if not args.no_graph:
-        graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
-            for i in range(G):
+            for i in range(C):
                 step(i)
             torch.cuda.synchronize()
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(G):
-                    step(i)
-    # at least --steps steps, in at least MIN_REPLAYS replays of G steps each
-    reps = max(MIN_REPLAYS, -(-args.steps // G))
+            for j in range(n_graphs):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for i in range(j * G, (j + 1) * G):
+                        step(i)
+                graphs.append(graph)
     steps = reps * G
-    step_bytes = sum(layers.step_bytes(i % args.layers, touched[i % n_draws]) for i in range(G)) / G + act_bytes
-    mean_uniq = sum(len(touched[i % n_draws]) for i in range(G)) / G
+    timed = [(r % n_graphs) * G + i for r in range(reps) for i in range(G)]      # cycle positions timed
+    step_bytes = sum(layers.step_bytes(i % args.layers, touched[i % n_draws]) for i in timed) / steps + act_bytes
+    mean_uniq = sum(len(touched[i % n_draws]) for i in timed) / steps
+    counter = [0]
 
     def replay():
-        if graph is not None:
-            graph.replay()
+        j = counter[0] % n_graphs
+        counter[0] += 1
+        if graphs:
+            graphs[j].replay()
         else:
-            for i in range(G):
+            for i in range(j * G, (j + 1) * G):
                 step(i)
 
-    ms, total_ms = timed_replays(torch, stream, replay, reps, max(1, -(-args.warmup // G)))
+    warm = max(1, -(-args.warmup // G))
+    warm += (-warm) % n_graphs                      # the timed replays start at the cycle's first graph
+    ms, total_ms = timed_replays(torch, stream, replay, reps, warm)
     st = replay_stats(ms, G)
     us_step = st["median_ms"] * 1e3
     gbps = step_bytes / (us_step * 1e-6) / 1e9
@@ -653,8 +726,10 @@ def run_layer(torch, args):
                                f"(BASELINE configs[{cfg_idx}])", "routing": args.routing,
                    "unique_experts_per_step": round(mean_uniq, 2),
                    "hidden": H, "inter": I, "experts": E, "shared": 1, "topk": TOPK, "tokens": T,
-                   "bits": None if prefill else args.bits, "layers_cycled": args.layers, "graph": graph is not None,
-                   "ksplit_gu": ws.shape.ksplit_gu, "ksplit_down": ws.shape.ksplit_down},
+                   "bits": None if prefill else args.bits, "layers_cycled": args.layers, "graph": bool(graphs),
+                   "graph_steps": G, "step_cycle": C,
+                   "ksplit_gu": ws.shape.ksplit_gu, "ksplit_down": ws.shape.ksplit_down,
+                   "mode": "strict" if strict_rows else "fast", "strict_rows": strict_rows},
         "step_bytes": int(step_bytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
         "kernel_us": {k: round(v, 3) for k, v in kt.items()},
         "roofline": roofline,
@@ -663,8 +738,19 @@ def run_layer(torch, args):
         result["kernel_us_note"] = "1 token: routing runs inside moe_gate_up (no prepare launch)"
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        what = f"step 0 of the timed sequence (layer 0, routing draw 0){'' if T == 1 else f', first token of {T}'}"
-        result["cpu_baseline"] = cpu_baseline(torch, layers, 0, x, logits[0], 1, 10.0, what)
+        if T == 1:
+            result["cpu_baseline"] = cpu_baseline(torch, layers, [0], x, [logits[0]], 1, 10.0,
+                                                  "step 0 of the timed sequence (layer 0, routing draw 0)")
+        elif not prefill:
+            # the whole step (every token, every expert they touch): one run after a warm-up decode
+            result["cpu_baseline"] = cpu_baseline(torch, layers, [0], x, [logits[0]], T, 10.0,
+                                                  "step 0 of the timed sequence (layer 0, routing draw 0)",
+                                                  runs=1, warmups=0)
+        else:
+            # a bounded sample of the prefill step: its first 32 tokens (about 25 s of CPU work)
+            result["cpu_baseline"] = cpu_baseline(torch, layers, [0], x, [logits[0]], 32, 10.0,
+                                                  "the first 32 tokens of step 0 (layer 0, routing draw 0) of 512",
+                                                  runs=1, warmups=0)
     return result
 
 
@@ -712,7 +798,7 @@ def run_stack(torch, args):
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
             step()
-    steps = max(MIN_REPLAYS, args.steps)       # one replay = one step through the L layers
+    steps = max(1, args.steps)                 # one replay = one step through the L layers
 
     ms, total_ms = timed_replays(torch, stream, graph.replay, steps, max(1, min(args.warmup, 5)))
     st = replay_stats(ms, 1)
@@ -751,8 +837,10 @@ def run_stack(torch, args):
         result["kernel_us_note"] = "1 token: routing runs inside moe_gate_up (no prepare launch)"
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(torch, layers, 0, h0, logits[0], 1, 10.0,
-                                              "layer 0 of the stacked step, first token of 8")
+        # time 2 layers of the step and scale by L / 2
+        result["cpu_baseline"] = cpu_baseline(torch, layers, [0, 1], h0, [logits[0], logits[1]], T, 10.0,
+                                              f"layers 0 and 1 of the stacked step, all {T} tokens (x{L // 2} "
+                                              f"for the {L}-layer step)", runs=1, warmups=0, scale=L / 2)
     return result
 
 
