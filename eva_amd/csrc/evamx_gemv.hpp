@@ -374,6 +374,124 @@ __device__ __forceinline__ void gemv_wave(const uint32_t* __restrict__ trellis, 
         if (kt + d < kt1) step(kt + d, ring[d]);
 }
 
+// ---------------------------------------------------------------------------------------------
+// The same decode GEMV with the products on the matrix cores: v_mfma_f32_4x4x4_16b_f16 runs 16
+// independent 4x4x4 blocks, block b on lanes 4b..4b+3, and the decode layout's lane quads are
+// exactly such blocks (the four lanes of a quad own four columns of one tile at the same k).
+// Lane 4b + j supplies column j of its block as the B operand (the four k of a k-group from its
+// decoded pairs) and row j of the block's A operand (the activations of row 4g + j of its 4-row
+// group at those k); the block's D holds the four rows of the lane's column in four registers.
+// One MFMA thus takes the products of 4 rows x 4 k per lane where v_dot2 takes 1 row x 2 k:
+// a k-slice costs 8 MFMAs per 4-row group instead of 16 v_dot2 per row. Rows of a group past the
+// call's rows read a copy of the group's first row (their outputs are dropped); a row's result
+// does not depend on the other rows of its group.
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+
+// Activation rows of the MFMA-product GEMV, staged in LDS: row m at base + m * row_words (a
+// padded stride, so that the four rows a lane quad reads sit in different banks), k-slice kt at
+// word 8 * (kt - kt0). Lane l reads row 4g + (l & 3) of group g.
+template <int NG>
+struct XLds4 {
+    const uint32_t* base;
+    int off[NG];            // this lane's row offset (words) in each group
+    int kt0;
+    __device__ __forceinline__ void init(const uint32_t* b, int row_words, int k0, int tm)
+    {
+        base = b;
+        kt0 = k0;
+        const int j = threadIdx.x & 3;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int m = 4 * g + j;
+            off[g] = (m < tm ? m : 4 * g < tm ? 4 * g : 0) * row_words;
+        }
+    }
+    __device__ __forceinline__ void load(int g, int kt, uint32_t (&d)[8]) const
+    {
+        const uint32_t* xp = (const uint32_t*)__builtin_assume_aligned(base + off[g] + 8 * (kt - kt0), 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = xp[i];
+    }
+};
+
+// B operand of one MFMA: column c (0: q, 1: q + 8) of the lane, k-group kg (k = 4 kg .. 4 kg + 3)
+// of the slice's decoded pairs (wp[4u + 2c + kh] holds k = 8 kh + 2u, 8 kh + 2u + 1).
+__device__ __forceinline__ half4_t m4_b(const half2_t (&wp)[16], int c, int kg)
+{
+    const int kh = kg >> 1, u = 2 * (kg & 1);
+    const half2_t lo = wp[4 * u + 2 * c + kh], hi = wp[4 * (u + 1) + 2 * c + kh];
+    return half4_t{lo.x, lo.y, hi.x, hi.y};
+}
+
+__device__ __forceinline__ half4_t m4_a(const uint32_t (&a)[8], int kg)
+{
+    const half2_t lo = __builtin_bit_cast(half2_t, a[2 * kg]), hi = __builtin_bit_cast(half2_t, a[2 * kg + 1]);
+    return half4_t{lo.x, lo.y, hi.x, hi.y};
+}
+
+// acc[g][c][i] += sum_k X[4g + i][k] * h_k over the wave's k-range [kt0, kt1) for the lane's column
+// c; groups g with 4g >= tm are skipped. Same ring, decode and prologue protocol as gemv_wave.
+template <int K2, int NG, int PF = 4, typename Pro>
+__device__ __forceinline__ void gemv_wave_m4(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
+                                             const XLds4<NG>& xs, int tm, f32x4v_t (&acc)[NG][2], Pro& prologue)
+{
+    using R = Rate<K2>;
+    constexpr int K = R::K;
+    constexpr int TW = R::TW;
+    const int lane = threadIdx.x & 63;
+    kt0 = __builtin_amdgcn_readfirstlane(kt0);
+    kt1 = __builtin_amdgcn_readfirstlane(kt1);
+    const uint32_t slice = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(nt_n * TW));
+    const uint32_t cbase = __builtin_amdgcn_readfirstlane(4u * (uint32_t)(cg * 8 * TW));
+    const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(trellis);
+    uint32_t lane_off, prev_off, sh;
+    lane_offsets<K2>(lane, lane_off, prev_off, sh);
+
+    prologue.issue();
+    LaneWords<K> ring[PF];
+    const int last = kt1 - 1;
+#pragma unroll
+    for (int d = 0; d < PF; ++d) load_slice<K>(ring[d], rsrc, cbase + (uint32_t)min(kt0 + d, last) * slice, lane_off, prev_off);
+    if constexpr (Pro::kWork) __builtin_amdgcn_sched_barrier(0);
+    prologue.finish();
+
+    // a step reads its slice's activations from LDS first: the decode hides their latency
+    auto step = [&](int kt, LaneWords<K>& w) {
+        uint32_t xa[NG][8];
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+            if (4 * g < tm) xs.load(g, kt, xa[g]);
+        half2_t wp[16];
+        decode_slice<K2>(w, sh, wp);
+        load_slice<K>(w, rsrc, cbase + (uint32_t)min(kt + PF, last) * slice, lane_off, prev_off);
+#pragma unroll
+        for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                if (4 * g < tm) {
+                    const half4_t a = m4_a(xa[g], kg);
+#pragma unroll
+                    for (int c = 0; c < 2; ++c)
+                        acc[g][c] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, m4_b(wp, c, kg), acc[g][c], 0, 0, 0);
+                }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int n_kt = kt1 - kt0;
+    int kt = kt0;
+    for (; kt + PF <= kt1; kt += PF) {
+        progress_priority(kt - kt0, n_kt);
+#pragma unroll
+        for (int d = 0; d < PF; ++d) step(kt + d, ring[d]);
+    }
+    progress_priority(n_kt, n_kt);
+#pragma unroll
+    for (int d = 0; d < PF - 1; ++d)
+        if (kt + d < kt1) step(kt + d, ring[d]);
+}
+
 // GEMV for a chunk of tm rows over the 128-element k-chunks [c0, c1) with the smallest
 // template that fits; writes fp32 partials part[slot_of[m] * part_stride + column] =
 // sum_k x_k w_k = 0x1eee * sum_k x_k h_k + 0xc931 * sum_k x_k.

@@ -234,12 +234,12 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events = nullptr);
 // last kernel's end timestamps (nullptr: none).
 void launch_router_front(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 void launch_prepare(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
-// Decode-path gate/up: tmax 1 the one-row launch that routes inside, 2 chunks in passes of up to
-// 2 rows, 8 up to 8 rows per pass (falls back to 2-row passes when the column groups are not a
-// multiple of the workgroup's 4 waves).
+// Decode-path gate/up and down (products on the matrix cores): tmax 1 the one-row launches (gate/up
+// routes inside), 2 chunks in passes of up to 4 rows, 8 up to 8 rows per pass (gate/up falls back
+// to 2-row passes when the column groups are not a multiple of the workgroup's 4 waves).
 void launch_gate_up_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 void launch_gate_up_decode8(const MoeParams& p, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
-void launch_gate_up_decode2(const MoeParams& p, bool group, dim3 grid, hipStream_t stream, hipEvent_t start,
+void launch_gate_up_decode4(const MoeParams& p, bool group, dim3 grid, hipStream_t stream, hipEvent_t start,
                             hipEvent_t stop);
 void launch_down_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop);

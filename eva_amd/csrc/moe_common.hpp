@@ -699,4 +699,14 @@ __device__ __forceinline__ const void* expert_ptr(const MoeParams& p, int e, int
     return (const void*)p.tables[(size_t)row * p.tbl_stride + e];
 }
 
+// Slots slot[0..tm) of a unit record (entries past tm repeat slot[0]); the record is not written
+// during the GEMV launch, so these are scalar loads.
+template <int TM>
+__device__ __forceinline__ void record_slots(const int* slot, int tm, int (&so)[TM])
+{
+    const __attribute__((address_space(4))) int* sl = (const __attribute__((address_space(4))) int*)slot;
+#pragma unroll
+    for (int m = 0; m < TM; ++m) so[m] = __builtin_amdgcn_readfirstlane(sl[m < tm ? m : 0]);
+}
+
 }  // namespace evamx

@@ -1,6 +1,6 @@
 // Gate/up launches of the decode path. This unit holds the one-row launch (routing inside it);
-// the 2-row and 8-row kernels sit in translation units of their own (moe_gate_up2.hip,
-// moe_gate_up8.hip) so that their instantiations compile in parallel.
+// the multi-row kernels sit in translation units of their own (moe_gate_up2.hip, moe_gate_up8.hip)
+// so that their instantiations compile in parallel.
 #include "moe_gate_up.hpp"
 
 namespace evamx {
@@ -20,8 +20,7 @@ void launch_gate_up_decode(const MoeParams& p, int tmax, hipStream_t stream, hip
     } else if (tmax == 8 && group) {
         launch_gate_up_decode8(p, grid, stream, start, stop);
     } else {
-        // chunks of up to 8 rows without the workgroup's shared LDS rows run in 2-row passes
-        launch_gate_up_decode2(p, group, grid, stream, start, stop);
+        launch_gate_up_decode4(p, group, grid, stream, start, stop);
     }
 }
 

@@ -1,6 +1,7 @@
 // Gate/up GEMV kernels of the decode path (calls of 1-2 rows, and strict calls): each wave
-// rotates its own inputs into LDS and streams its weights (moe_gate_up.hip instantiates the 1- and
-// 2-row kernels, moe_gate_up8.hip the 8-row one).
+// rotates its own inputs into LDS and streams its weights, the products on the matrix cores
+// (moe_gate_up.hip instantiates the one-row kernel, moe_gate_up2.hip the 2- and 4-row ones,
+// moe_gate_up8.hip the 8-row one).
 #pragma once
 #include "moe_common.hpp"
 
@@ -147,19 +148,28 @@ struct RotStageGroup {
     }
 };
 
+// Words of an LDS row of rotated inputs: ROT_CW chunks, padded so that the four rows a lane quad
+// reads start in different banks.
+constexpr int ROT_ROW_WORDS = ROT_CW * 64 + 8;
+
 // Gate/up GEMV of tm rows (slots slot[0..tm)) over the 128-chunks [c0, c1): each window of at
 // most ROT_CW chunks is rotated into LDS (GROUP: by the workgroup's four waves together), then
-// streamed; writes the fp32 partials of the rows.
+// streamed with the products on the matrix cores (gemv_wave_m4, rows in groups of four); writes
+// the fp32 partials of the rows.
 template <int K2, int TM, bool GROUP, int NW = ROT_WAVES>
 __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                  const int (&so)[TM], int tm, int cg, int c0, int c1, float* part,
                                                  uint32_t* lds, float* lsums)
 {
     const int lane = threadIdx.x & 63;
-    float acc[TM][2], xs[TM];
+    constexpr int NG = (TM + 3) / 4;
+    f32x4v_t acc[NG][2];
+    float xs[TM];
 #pragma unroll
-    for (int m = 0; m < TM; ++m) acc[m][0] = acc[m][1] = xs[m] = 0.0f;
-    constexpr int RW = ROT_CW * 64;
+    for (int g = 0; g < NG; ++g) acc[g][0] = acc[g][1] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < TM; ++m) xs[m] = 0.0f;
+    constexpr int RW = ROT_ROW_WORDS;
     const int slots = p.T * p.topk;
     __amdgpu_buffer_rsrc_t xrs[TM];
 #pragma unroll
@@ -169,17 +179,18 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
     }
     const __amdgpu_buffer_rsrc_t srs = weight_rsrc((const uint32_t*)suh);
     auto window = [&](int w0, int w1) {
-        const XLds src{lds, RW, 8 * w0};
+        XLds4<NG> src;
+        src.init(lds, RW, 8 * w0, tm);
         if constexpr (GROUP) {
             RotStageGroup<TM, NW> stage{p, so, tm, w0, w1, RW, lane, (int)(threadIdx.x >> 6), srs, {}, lds, lsums, xs};
 #pragma unroll
             for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
-            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+            gemv_wave_m4<K2, NG>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
         } else {
             RotStage<TM> stage{p, so, tm, w0, w1, RW, lane, srs, {}, lds, xs};
 #pragma unroll
             for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
-            gemv_wave<K2, TM>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+            gemv_wave_m4<K2, NG>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
         }
     };
     if (c1 - c0 <= ROT_CW) {
@@ -197,48 +208,25 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
     for (int m = 0; m < TM; ++m) {
         if (m < tm) {
             float* dst = part + (size_t)so[m] * p.I;
-            dst[col0] = mul1_affine(acc[m][0], xs[m]);
-            dst[col1] = mul1_affine(acc[m][1], xs[m]);
+            dst[col0] = mul1_affine(acc[m / 4][0][m % 4], xs[m]);
+            dst[col1] = mul1_affine(acc[m / 4][1][m % 4], xs[m]);
         }
     }
 }
 
-// Slots slot[0..tm) of a unit record (entries past tm repeat slot[0]); the record is not written
-// during the GEMV launch, so these are scalar loads.
-template <int TM>
-__device__ __forceinline__ void record_slots(const int* slot, int tm, int (&so)[TM])
-{
-    const __attribute__((address_space(4))) int* sl = (const __attribute__((address_space(4))) int*)slot;
-#pragma unroll
-    for (int m = 0; m < TM; ++m) so[m] = __builtin_amdgcn_readfirstlane(sl[m < tm ? m : 0]);
-}
-
-template <int K2, int TM, bool GROUP>
-__device__ __forceinline__ void gate_up_rot_rec(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
-                                                const int* slot, int tm, int cg, int c0, int c1, float* part,
-                                                uint32_t* lds, float* lsums)
-{
-    int so[TM];
-    record_slots<TM>(slot, tm, so);
-    gate_up_rot_rows<K2, TM, GROUP>(p, trellis, suh, so, tm, cg, c0, c1, part, lds, lsums);
-}
-
-// tm rows (at most TMAX) through the smallest compiled row count that holds them; every row's
-// arithmetic is the same whatever that count (rows are independent accumulators).
+// tm rows (at most TMAX; slots slot[0..tm) of a unit record) through one TMAX-row variant per rate
+// (rows past tm are skipped): the kernel's register budget is its widest variant's anyway, every
+// smaller variant as well would make its compile several times longer, and every row's arithmetic
+// is the same whatever the variant (rows are independent accumulators).
 template <int K2, int TMAX, bool GROUP>
 __device__ __forceinline__ void gate_up_rot_fit(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                 const int* slot, int tm, int cg, int c0, int c1, float* part,
                                                 uint32_t* lds, float* lsums)
 {
-    static_assert(TMAX == 1 || TMAX == 2 || TMAX == 8, "decode path rows: 1, 2 or 8 per pass");
-    if constexpr (TMAX == 1) {
-        gate_up_rot_rec<K2, 1, GROUP>(p, trellis, suh, slot, tm, cg, c0, c1, part, lds, lsums);
-    } else {
-        // one TMAX-row variant per rate (rows past tm are skipped): the kernel's register budget is
-        // its widest variant's anyway, and every smaller variant as well would make its compile
-        // several times longer
-        gate_up_rot_rec<K2, TMAX, GROUP>(p, trellis, suh, slot, tm, cg, c0, c1, part, lds, lsums);
-    }
+    static_assert(TMAX == 1 || TMAX == 2 || TMAX == 4 || TMAX == 8, "decode path rows: 1, 2, 4 or 8 per pass");
+    int so[TMAX];
+    record_slots<TMAX>(slot, tm, so);
+    gate_up_rot_rows<K2, TMAX, GROUP>(p, trellis, suh, so, tm, cg, c0, c1, part, lds, lsums);
 }
 
 template <int K2, int TMAX, bool GROUP>
@@ -265,7 +253,7 @@ __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint3
 template <int TMAX, bool GROUP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_rot_kernel(MoeParams p)
 {
-    __shared__ uint32_t xl[GROUP ? 1 : 4][TMAX * ROT_CW * 64];
+    __shared__ uint32_t xl[GROUP ? 1 : 4][TMAX * ROT_ROW_WORDS];
     __shared__ float xsums[TMAX * ROT_CW];
     const int wave = threadIdx.x >> 6;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
@@ -448,7 +436,7 @@ __device__ __forceinline__ void publish_routes1(const MoeParams& p, int lane)
 template <bool GROUP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_route1_kernel(MoeParams p)
 {
-    __shared__ uint32_t xl[GROUP ? 1 : 4][ROT_CW * 64];
+    __shared__ uint32_t xl[GROUP ? 1 : 4][ROT_ROW_WORDS];
     __shared__ float xsums[ROT_CW];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (blockIdx.x == gridDim.x - 1) {
