@@ -146,6 +146,9 @@ class DeviceLayers:
     def gate_up_bytes(self, l, experts):
         return sum(2 * proj_bytes(H, I, self.rates[l][e]) for e in list(experts) + [self.n - 1])
 
+    def down_bytes(self, l, experts):
+        return sum(proj_bytes(I, H, self.rates[l][e]) for e in list(experts) + [self.n - 1])
+
 
 def cpu_info(torch):
     """Host description for the CPU baseline: lscpu's model name, torch version and threading."""
@@ -713,7 +716,15 @@ def run_layer(torch, args):
     else:
         roofline["decode_alu_ceiling"] = decode_ceiling(ops, (args.bits,), roofline["achieved"])
         if T == 1 and args.bits == 4.0:
-            roofline["read_floor"] = read_floor(torch, ops, H, I, TOPK + 1, roofline["achieved"])
+            roofline["read_floor"] = read_floor(torch, ops, H, I, TOPK + 1, 2, roofline["achieved"])
+            # the down launch beside it: its own bytes, decode ceiling and read floor
+            d_bytes = sum(layers.down_bytes(i % args.layers, touched[i % n_draws]) for i in range(n_ev)) / n_ev
+            d_ach = d_bytes / (kt["moe_down"] * 1e-6) / 1e9
+            ceil = roofline["decode_alu_ceiling"]["value"]
+            roofline["down"] = {"kernel": "moe_down", "achieved": round(d_ach, 1), "peak": PEAK_HBM, "unit": "GB/s",
+                                "frac": round(d_ach / PEAK_HBM, 4), "algorithmic_bytes_per_launch": int(d_bytes),
+                                "avg_launch_us": round(kt["moe_down"], 3), "decode_alu_ceiling_frac": round(d_ach / ceil, 4),
+                                "read_floor": read_floor(torch, ops, I, H, TOPK + 1, 1, d_ach)}
     cfg_idx = 3 if prefill else (1 if T == 1 else 2)
     rates = "per-expert rates {2,3,4,5} (shared 4)" if prefill else f"{args.bits:g} bpw"
     result = {
@@ -957,19 +968,20 @@ def decode_ceiling(ops, bits_list, achieved_gbps=None, weights=None):
     return out
 
 
-def read_floor(torch, ops, H, I, units, achieved_gbps):
-    """Memory-side bound of the one-row gate/up launch (evamx_bench_read): the launch's own bytes
+def read_floor(torch, ops, n_in, n_out, units, nproj, achieved_gbps):
+    """Memory-side bound of a one-row decode GEMV launch (evamx_bench_read): the launch's own bytes
     in its own shape, without the decode. One-row calls aim their k-split at two waves per SIMD:
-    units x (gate, up) x I/128 column groups x ks waves, ks = that target over the per-split
-    items, each wave streaming the 8 * (H/128 / ks) k-slices of its split as 1 KiB chunks (8 tiles
-    at 4 bits), four in flight. Back-to-back launches over distinct copies of at least 1 GiB in
-    total (a repeated 132 MB buffer would be served partly by the Infinity Cache), so the figure
-    includes each launch's ramp and tail but only part of the gap between launches."""
-    ncg = I // 128
-    per_split = units * 2 * ncg
+    units x nproj (gate/up: 2, down: 1) x n_out/128 column groups x ks waves, ks = that target over
+    the per-split items, each wave streaming the 8 * (n_in/128 / ks) k-slices of its split as 1 KiB
+    chunks (8 tiles at 4 bits), four in flight. Back-to-back launches over distinct copies of at
+    least 1 GiB in total (a repeated buffer of this size would be served partly by the Infinity
+    Cache), so the figure includes each launch's ramp and tail but only part of the gap between
+    launches."""
+    ncg = n_out // 128
+    per_split = units * nproj * ncg
     waves_target = torch.cuda.get_device_properties(0).multi_processor_count * 16 // 2
     ks = max(1, waves_target // per_split)
-    rows = 8 * ((H // 128) // ks)
+    rows = 8 * ((n_in // 128) // ks)
     waves = per_split * ks
     bps = ops.read_floor(ncg, rows, waves)
     return {"kernel": "evamx_bench_read", "unit": "GB/s", "value": round(bps / 1e9, 1),

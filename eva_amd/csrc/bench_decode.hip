@@ -1,8 +1,9 @@
 // Decode ALU ceiling: the rate at which gfx950 evaluates the EXL3 trellis decode of the GEMV
-// (window funnels, MUL1 hashes, byte sums into fp16 pairs, one fp16 dot product per pair)
-// when nothing is loaded from memory. Every lane decodes one k-slice's 32 positions per
-// iteration from register-resident words, which it then advances, exactly the per-weight
-// instruction mix of the decode GEMV's inner loop for one row. Bench.py divides the trellis
+// (window funnels, MUL1 hashes, byte sums into fp16 pairs) with its matrix-core products (eight
+// v_mfma_f32_4x4x4_16b_f16 per k-slice and row group) when nothing is loaded from memory. Every
+// lane decodes one k-slice's 32 positions per iteration from register-resident words, which it
+// then advances, exactly the per-weight instruction mix of the decode GEMV's inner loop for one
+// row group (gemv_wave_m4, without its LDS activation reads). Bench.py divides the trellis
 // bytes this rate implies into a GEMV's achieved bytes to say how close the GEMV is to the
 // arithmetic bound, as opposed to the HBM bound.
 //
@@ -22,21 +23,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void b
 #pragma unroll
     for (int i = 0; i <= R::K; ++i) w.b[i] = 0x9E3779B9u * (threadIdx.x + 7u * i + 1u) + blockIdx.x;
     const uint32_t sh = (threadIdx.x & 1) ? 0u : 16u;
-    float a0 = 0.0f, a1 = 0.0f;
-    const half2_t x = {(half_t)0.5f, (half_t)-0.25f};
+    f32x4v_t acc[2] = {f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    const half4_t x = {(half_t)0.5f, (half_t)-0.25f, (half_t)0.125f, (half_t)1.0f};
     for (int it = 0; it < iters; ++it) {
         half2_t wp[16];
         decode_slice<K2>(w, sh, wp);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            a0 = dot2(wp[2 * u], x, a0);
-            a1 = dot2(wp[2 * u + 1], x, a1);
-        }
+        for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[c] = __builtin_amdgcn_mfma_f32_4x4x4f16(x, m4_b(wp, c, kg), acc[c], 0, 0, 0);
 #pragma unroll
         for (int i = 0; i <= R::K; ++i) w.b[i] += 0x7F4A7C15u * (i + 1);
     }
     // keep the work observable without storing per lane
-    if (a0 + a1 == 1234.5f) sink[threadIdx.x] = a0;
+    if (acc[0][0] + acc[1][1] == 1234.5f) sink[threadIdx.x] = acc[0][2];
 }
 
 // Wave w = (chain, cg), cg = w % ncg: the wave's 64 lanes read 16 bytes each from row

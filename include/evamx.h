@@ -222,8 +222,9 @@ const void* evamx_moe_rotated_ptr(const evamx_moe_shape* shape, void* workspace)
 
 /* No counterpart in the reference: a benchmark kernel for the arithmetic bound of the decode
  * GEMV. `waves` waves each decode `iters` k-slices (32 weights per lane) of register-resident
- * trellis words at rate `bits` with one fp16 dot product per weight pair, the GEMV's
- * per-weight instruction mix without its memory traffic; time it with events on `stream`.
+ * trellis words at rate `bits` with the GEMV's matrix-core products (eight 4x4x4 MFMA blocks per
+ * slice and row group), the GEMV's per-weight instruction mix without its memory traffic; time
+ * it with events on `stream`.
  * Weights decoded = waves * 64 * 32 * iters. sink: device float[256] (written only to keep the
  * work observable). */
 int evamx_bench_decode(float bits, int waves, int iters, float* sink, evamx_stream_t stream);

@@ -45,6 +45,61 @@ def _run(ops, dev, case, x, logits, static, rows_max=ROWS_MAX):
     return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
 
 
+def test_static_forward_captured_in_a_graph(dev, case):
+    """The entry point as the callers it is for use it: static forwards of 1, 2 and 16 rows (the
+    one-row launch that routes inside, the two-row decode path, the 16-row MFMA tiles) captured
+    into one hipGraph. First in this file, so that in a fresh process the per-device set-up
+    (symbol lookup and the flag word's fill kernel) happens under capture. Three replays, with
+    eager static calls of other sizes in between that overwrite the scratch, each equal bit for
+    bit to the eager static calls and to the workspace path on the same inputs."""
+    from eva_amd import ops
+    experts, shared, de, ds = case
+    rng = np.random.default_rng(811)
+    shape = ops.MoeShape(ROWS_MAX, H, I, TOPK, E, 1, 0, 0, 0)
+    calls = []
+    for rows in (1, 2, 16):
+        x = to_dev(synth.activations_bf16(rng, rows, H), dev).to(torch.bfloat16)
+        z = to_dev(synth.logits_skewed(rng, rows, E, hot=1, warm=3), dev)
+        bufs = dict(sel=torch.empty(rows, TOPK, dtype=torch.int64, device=dev),
+                    weights=torch.empty(rows, TOPK, dtype=torch.float32, device=dev))
+        out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+        calls.append((x, z, bufs, out))
+
+    def run_all():
+        for x, z, bufs, out in calls:
+            ops.moe_forward_static(shape, x, de.table, out, limit=0.75, bits=4, logits=z, shared_ptrs=ds.ptrs(0),
+                                   shared_bits=4, **bufs)
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run_all()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    graph_out = [out.clone() for _, _, _, out in calls]
+    for _, _, _, out in calls:
+        out.fill_(float("nan"))
+    run_all()                                                     # eager static calls
+    torch.cuda.synchronize()
+    for (x, z, bufs, out), got in zip(calls, graph_out):
+        assert torch.equal(out.view(torch.int32), got.view(torch.int32))
+        ws = ops.MoeWorkspace(dev, rows_max=ROWS_MAX, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True)
+        want = torch.empty_like(out)
+        ops.moe_forward(ws, x, de.table, want, limit=0.75, bits=4, logits=z, shared_ptrs=ds.ptrs(0), shared_bits=4,
+                        sel=torch.empty_like(bufs["sel"]), weights=torch.empty_like(bufs["weights"]))
+        torch.cuda.synchronize()
+        assert torch.equal(want.view(torch.int32), got.view(torch.int32))
+    other = synth.activations_bf16(rng, 5, H)
+    for rows in (5, 3, 9):                                        # eager work on the scratch between replays
+        _run(ops, dev, case, other[:min(rows, 5)], synth.logits_plain(rng, min(rows, 5), E), static=True)
+        for _, _, _, out in calls:
+            out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for (_, _, _, out), got in zip(calls, graph_out):
+            assert torch.equal(out.view(torch.int32), got.view(torch.int32))
+
+
 def test_static_scratch_matches_workspace_twice(dev, case):
     from eva_amd import ops
     experts, shared, _, _ = case
