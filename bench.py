@@ -456,7 +456,7 @@ def parse_args():
                     help="print the markdown summary of rocprofv3 --pmc counter_collection.csv files and exit")
     ap.add_argument("--calibration", metavar="CSV", nargs="*", default=[],
                     help="with --summarize-pmc: the counter CSVs of a --copy-calibration run")
-    ap.add_argument("--traffic-key", default=None, help="with --summarize-pmc: e.g. tokens=1,bits=4")
+    ap.add_argument("--traffic-key", default=None, help="with --summarize-pmc: e.g. tokens=1,bits=4,mode=strict")
     ap.add_argument("--summarize-counters", metavar="CSV", nargs="+",
                     help="print per-kernel averages of any rocprofv3 --pmc counters and exit (no GPU)")
     ap.add_argument("--skip-dispatches", type=int, default=0, help="with --summarize-trace: warm-up dispatches")
@@ -704,7 +704,8 @@ def run_layer(torch, args):
     kt = kernel_times(torch, stream, step, n_ev, skip=2 if prefill else 8,
                       kernelless=("moe_prepare",) if T == 1 else ())
     gu_bytes_launch = sum(layers.gate_up_bytes(i % args.layers, touched[i % n_draws]) for i in range(n_ev)) / n_ev
-    roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, args.bits))
+    roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"],
+                                measured_traffic(T, args.bits, "strict" if strict_rows else "fast"))
     if prefill:
         roofline["decode_alu_ceiling"] = decode_ceiling(ops, (2.0, 3.0, 4.0, 5.0))
         # MFMA utilisation of the gate/up GEMM: 2 * H * I flops per row and projection
@@ -779,8 +780,9 @@ def run_stack(torch, args):
     logits = torch.randn((L, T, E), generator=g, device=dev)
     h0 = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
     h = h0.clone()
+    strict_rows = strict_rows_for(args.mode, T)
     ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
-                          ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down)
+                          ksplit_gu=args.ksplit_gu, ksplit_down=args.ksplit_down, strict_rows=strict_rows)
     sels = torch.empty(L, T, TOPK, dtype=torch.int64, device=dev)
     wts = torch.empty(L, T, TOPK, dtype=torch.float32, device=dev)
 
@@ -826,7 +828,7 @@ def run_stack(torch, args):
 
     kt = kernel_times(torch, stream, lambda i, events=None: layer(i % L, events), L, skip=0)
     gu_bytes_launch = sum(layers.gate_up_bytes(l, touched[l]) for l in range(L)) / L
-    roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, K))
+    roofline = gate_up_roofline(gu_bytes_launch, kt["moe_gate_up"], measured_traffic(T, K, "strict" if strict_rows else "fast"))
     roofline["decode_alu_ceiling"] = decode_ceiling(ops, (K,), roofline["achieved"])
     result = {
         "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
@@ -839,7 +841,7 @@ def run_stack(torch, args):
                    "layers": L, "tokens": T, "bits": K, "resident_weight_gb": round(layers.trellis.numel() * 2 / 1e9, 2),
                    "unique_experts_per_layer": round(mean_uniq, 2), "down_svh_scale": STACK_DOWN_SCALE,
                    "residual_max_abs": round(h_max, 3), "hidden": H, "inter": I, "experts": E,
-                   "shared": 1, "topk": TOPK},
+                   "shared": 1, "topk": TOPK, "mode": "strict" if strict_rows else "fast", "strict_rows": strict_rows},
         "step_bytes": int(step_bytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
         "kernel_us": {k: round(v, 3) for k, v in kt.items()},
         "roofline": roofline,
@@ -1007,17 +1009,18 @@ def copy_calibration(torch):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_gate_up_traffic_dsv3.md")
 
 
-def measured_traffic(tokens, bits):
+def measured_traffic(tokens, bits, mode):
     """HBM bytes per moe_gate_up launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration), or None if this workload has
-    not been profiled."""
+    not been profiled in this mode (1-token calls run the same kernels in both modes)."""
     import re
     try:
         text = open(TRAFFIC_FILE).read()
     except OSError:
         return None
     key = "mixed" if bits is None else f"{bits:g}"
-    m = re.search(rf"^traffic_bytes_per_launch\[tokens={tokens},bits={key}\]:\s*(\d+)", text, flags=re.M)
+    mode = "strict" if tokens == 1 else mode
+    m = re.search(rf"^traffic_bytes_per_launch\[tokens={tokens},bits={key},mode={mode}\]:\s*(\d+)", text, flags=re.M)
     return int(m.group(1)) if m else None
 
 
