@@ -180,27 +180,30 @@ __global__ __launch_bounds__(256) void lin_epilogue_kernel(LinParams p)
     const int ncg = p.out / 128;
     if (wid >= ncg * p.rows) return;
     const int m = wid / ncg, cg = wid % ncg;
-    float sv[2];
+    float sv[2];                                       // loaded with the partials
 #pragma unroll
     for (int h = 0; h < 2; ++h) sv[h] = h2f(p.svh[cg * 128 + lane_col(lane, h)]);
-    // the k-split partials in fixed order, loads of up to 8 splits issued before their adds
-    float v[2];
+    // the k-split partials in fixed order; the loads of up to 16 splits of both columns are issued
+    // before their adds (one memory round trip per 16 splits: the call is latency-bound)
+    float v[2] = {0.0f, 0.0f};
     const size_t stride = (size_t)p.rows * p.out;
+    const float* pp[2] = {p.part + (size_t)m * p.out + cg * 128 + lane_col(lane, 0),
+                          p.part + (size_t)m * p.out + cg * 128 + lane_col(lane, 1)};
+    for (int q0 = 0; q0 < p.ks; q0 += 16) {
+        float t[2][16];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const float* pp = p.part + (size_t)m * p.out + cg * 128 + lane_col(lane, h);
-        float acc = 0.0f;
-        for (int q0 = 0; q0 < p.ks; q0 += 8) {
-            float t[8];
+        for (int i = 0; i < 16; ++i)
+            if (q0 + i < p.ks)
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (q0 + i < p.ks) t[i] = gptr<float>(pp)[(q0 + i) * stride];
+                for (int h = 0; h < 2; ++h) t[h][i] = gptr<float>(pp[h])[(q0 + i) * stride];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (q0 + i < p.ks) acc += t[i];
-        }
-        v[h] = h2f(f2h(acc));                          // C in fp16
+        for (int i = 0; i < 16; ++i)
+            if (q0 + i < p.ks)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) v[h] += t[h][i];
     }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) v[h] = h2f(f2h(v[h]));    // C in fp16
     had128_lane(v[0], v[1], lane);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {

@@ -709,4 +709,23 @@ __device__ __forceinline__ void record_slots(const int* slot, int tm, int (&so)[
     for (int m = 0; m < TM; ++m) so[m] = __builtin_amdgcn_readfirstlane(sl[m < tm ? m : 0]);
 }
 
+// A slot record through scalar loads (the records are written by an earlier launch and only read
+// after it), field by field. (One 16-dword vector load of the whole record failed the decode-path
+// parity tests, which pass with these per-field loads; its cause was not found.)
+__device__ __forceinline__ SlotRec load_slot_rec(const SlotRec* rp)
+{
+    const __attribute__((address_space(4))) SlotRec* c = (const __attribute__((address_space(4))) SlotRec*)rp;
+    SlotRec r;
+    r.active = c->active;
+    r.shared = c->shared;
+    r.s_gu = c->s_gu;
+    r.s_d = c->s_d;
+    r.w = c->w;
+    r.g_svh = c->g_svh;
+    r.u_svh = c->u_svh;
+    r.d_suh = c->d_suh;
+    r.d_svh = c->d_svh;
+    return r;
+}
+
 }  // namespace evamx

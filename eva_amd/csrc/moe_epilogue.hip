@@ -71,13 +71,13 @@ __global__ __launch_bounds__(256) void moe_act_kernel(MoeParams p)
     const half_t *g_svh, *u_svh, *d_suh;
     if constexpr (REC) {
         s = o;
-        const SlotRec* rp = p.srec + s;
-        if (!__builtin_amdgcn_readfirstlane(rp->active)) return;
-        shared = __builtin_amdgcn_readfirstlane(rp->shared) != 0;
-        Sg = __builtin_amdgcn_readfirstlane(rp->s_gu);
-        g_svh = (const half_t*)rp->g_svh;
-        u_svh = (const half_t*)rp->u_svh;
-        d_suh = (const half_t*)rp->d_suh;
+        const SlotRec rec = load_slot_rec(p.srec + s);
+        if (!rec.active) return;
+        shared = rec.shared != 0;
+        Sg = rec.s_gu;
+        g_svh = (const half_t*)rec.g_svh;
+        u_svh = (const half_t*)rec.u_svh;
+        d_suh = (const half_t*)rec.d_suh;
     } else {
         const int slots = p.T * p.topk;
         s = __builtin_amdgcn_readfirstlane(p.order[o]);
@@ -282,7 +282,8 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
 {
     __shared__ float part[EVAMX_MAX_TOPK + 1][128];
     __shared__ int active[EVAMX_MAX_TOPK + 1];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // uniform: the slot records load as scalars
     const int ncg = p.H / 128;
     const int row = blockIdx.x / ncg, cg = blockIdx.x % ncg;
     const int slots = p.T * p.topk;
@@ -296,14 +297,14 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
         int S;
         const half_t* svh;
         if constexpr (REC) {
-            const SlotRec* rp = p.srec + sk;
-            if (!__builtin_amdgcn_readfirstlane(rp->active)) {
+            const SlotRec rec = load_slot_rec(p.srec + sk);
+            if (!rec.active) {
                 if (lane == 0) active[k] = 0;
                 continue;
             }
-            w = rp->w;
-            S = __builtin_amdgcn_readfirstlane(rp->s_d);
-            svh = (const half_t*)rp->d_svh;
+            w = rec.w;
+            S = rec.s_d;
+            svh = (const half_t*)rec.d_svh;
         } else {
             const int le = shared ? -1 : __builtin_amdgcn_readfirstlane(p.local[sk]);
             const int mult = __builtin_amdgcn_readfirstlane(p.slot_mult[sk]);
@@ -317,12 +318,14 @@ __global__ __launch_bounds__(64 * EVAMX_COMBINE_WAVES) void moe_combine_kernel(M
                          : (const half_t*)p.tables[(size_t)EVAMX_TBL_D_SVH * p.tbl_stride + le];
             S = ks_of_chunk(ks_down(p, units), mult);
         }
+        // the scales (and the shared expert's gate) are loaded with the partials
+        const float s0 = h2f(svh[col0]), s1 = h2f(svh[col1]);
+        const float gv = shared && p.sh_gate_w ? p.gate_val[row] : 1.0f;
         float v[2];
         sum_partials(p, sk, cg, lane, S, v);
-        combine_item(shared, w, h2f(svh[col0]), h2f(svh[col1]), v, lane);
+        combine_item(shared, w, s0, s1, v, lane);
         if (shared && p.sh_gate_w) {
             // gated shared expert: gv * shared (exl3_moe_coop_kernel.cuh:942-948)
-            const float gv = p.gate_val[row];
             v[0] = gv * v[0];
             v[1] = gv * v[1];
         }
