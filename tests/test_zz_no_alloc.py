@@ -149,3 +149,37 @@ def test_static_refusals(dev, case):
     a.workspace = 1 << 20
     a.workspace_bytes = 1 << 20
     assert L.evamx_moe_forward_static(ctypes.byref(a), None) == _lib.EVAMX_EINVAL
+
+
+def test_static_strict_rows(dev, case):
+    """Strict mode on the fixed scratch: a 16-row static call with strict_rows 16 gives the bits of
+    the workspace path in strict mode, and each of its rows the bits of a one-row static call (the
+    strict property), then an 8-row call the bits of its own rows alone."""
+    from eva_amd import ops
+    experts, shared, de, ds = case
+    rng = np.random.default_rng(812)
+    kw = dict(limit=0.75, bits=4, shared_ptrs=ds.ptrs(0), shared_bits=4)
+
+    def static(x, z, strict_rows):
+        rows = x.shape[0]
+        out = torch.empty(rows, H, dtype=torch.float32, device=dev)
+        ops.moe_forward_static(ops.MoeShape(ROWS_MAX, H, I, TOPK, E, 1, 0, 0, strict_rows), x, de.table, out,
+                               logits=z, sel=torch.empty(rows, TOPK, dtype=torch.int64, device=dev),
+                               weights=torch.empty(rows, TOPK, dtype=torch.float32, device=dev), **kw)
+        torch.cuda.synchronize()
+        return out
+
+    for rows in (ROWS_MAX, 8):
+        x = to_dev(synth.activations_bf16(rng, rows, H), dev).to(torch.bfloat16)
+        z = to_dev(synth.logits_skewed(rng, rows, E, hot=1, warm=3), dev)
+        got = static(x, z, ROWS_MAX)
+        ws = ops.MoeWorkspace(dev, rows_max=ROWS_MAX, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
+                              strict_rows=ROWS_MAX)
+        want = torch.empty_like(got)
+        ops.moe_forward(ws, x, de.table, want, logits=z, sel=torch.empty(rows, TOPK, dtype=torch.int64, device=dev),
+                        weights=torch.empty(rows, TOPK, dtype=torch.float32, device=dev), **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32)), rows
+        for r in range(rows):
+            alone = static(x[r:r + 1], z[r:r + 1], ROWS_MAX)
+            assert torch.equal(alone.view(torch.int32), got[r:r + 1].view(torch.int32)), (rows, r)
