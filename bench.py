@@ -878,7 +878,7 @@ def run_stack(torch, args):
         result["kernel_us_note"] = "1 token: routing runs inside moe_gate_up (no prepare launch)"
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        # time 2 layers of the step and scale by L / 2
+        # the configuration's own work: 2 layers of the step, scaled by L / 2
         result["cpu_baseline"] = cpu_baseline(torch, layers, [0, 1], h0, [logits[0], logits[1]], T, 10.0,
                                               f"layers 0 and 1 of the stacked step, all {T} tokens (x{L // 2} "
                                               f"for the {L}-layer step)", runs=1, warmups=0, scale=L / 2)

@@ -3,8 +3,10 @@
 // GEMV lane layout (wave64): lane = 8*i + q streams tile (kt, 8*cg + i) words q*K..q*K+K-1 with
 // one vector load per k-slice and owns output columns 16i+q and 16i+q+8 of the 128-column group
 // for all 16 k of the tile, so the k-loop needs no cross-lane reduction and a wave's 128 columns
-// are exactly one Hadamard chunk. The 16 decoded k of a column pair up as (k, k+1) and meet the
-// activation pairs (x[2m], x[2m+1]) in v_dot2_f32_f16 with fp32 accumulation.
+// are exactly one Hadamard chunk. The 16 decoded k of a column pair up as (k, k+1). The MoE
+// decode path multiplies them on the matrix cores (gemv_wave_m4: each lane quad is one
+// v_mfma_f32_4x4x4_16b_f16 block); the single linear's GEMV meets the activation pairs
+// (x[2m], x[2m+1]) in v_dot2_f32_f16 (gemv_wave), both with fp32 accumulation.
 #pragma once
 #include "evamx_device.hpp"
 

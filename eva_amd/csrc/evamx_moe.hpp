@@ -14,7 +14,7 @@ constexpr int EVAMX_CHUNK = 8;             // slots of one expert per GEMV work 
 constexpr int EVAMX_TILE_ROWS = 64;        // slots of one expert per MFMA work item
 constexpr int EVAMX_SMALL_TILE_ROWS = 16;  // the same for calls of at most 16 tokens (16-row kernel)
 constexpr int EVAMX_MFMA_MIN_ROWS = 3;     // calls with at least this many rows take the MFMA path
-                                           // (one decode per tile beats per-row dot2 from 3 rows)
+                                           // (one decode per tile beats the decode GEMV from 3 rows)
 
 // Pointer-table rows, in the reference's order (ds41/cache.py:1877-1886).
 enum {
