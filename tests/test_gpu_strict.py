@@ -195,6 +195,48 @@ def test_strict_calls_above_the_bound_take_the_fast_path(dev):
     assert rel_err_rows(y12, ref) < TOL and rel_err_rows(y1, ref) < TOL
 
 
+def test_strict_router_front_no_shared(dev):
+    """Strict mode through the router front (logits from the fp32 gate weight inside the call),
+    sqrt-softplus scores with a selection bias, and no shared expert: every row of calls of 2, 6
+    and 11 tokens equals the row alone, bit for bit (routes, weights and output), and the oracle's
+    layer on the kernel's own logits within the tolerance."""
+    ops = _ops()
+    H, I, E, topk, rows = 512, 512, 24, 6, 11
+    rng = np.random.default_rng(79)
+    experts, _ = _small_case(rng, H, I, E)
+    de = DeviceExperts(experts, dev)
+    x = synth.activations_bf16(rng, rows, H)
+    gate_w = (rng.standard_normal((E, H)) / np.sqrt(H)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(E)).astype(np.float32)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=False,
+                          strict_rows=rows)
+    xd, gd, bd = to_dev(x, dev).to(torch.bfloat16), to_dev(gate_w, dev), to_dev(bias, dev)
+
+    def run(r0, T):
+        out = torch.empty(T, H, dtype=torch.float32, device=dev)
+        sel = torch.empty(T, topk, dtype=torch.int64, device=dev)
+        w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+        ops.moe_forward(ws, xd[r0:r0 + T], de.table, out, limit=10.0, bits=4.0, gate_w=gd, sel=sel, weights=w,
+                        score_fn="sqrt_softplus", sel_bias=bd)
+        torch.cuda.synchronize()
+        z = ws.logits(T, E).cpu().numpy().copy()
+        return out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy(), z
+
+    alone = [run(r, 1) for r in range(rows)]
+    z1 = np.concatenate([a[3] for a in alone])
+    ref = coop.moe_layer(x, z1, experts, None, topk, 10.0, score_fn="sqrt_softplus", sel_bias=bias)[0]
+    y1 = np.concatenate([a[0] for a in alone])
+    assert rel_err_rows(y1, ref) < TOL
+    for T in (2, 6, 11):
+        for r0 in sorted({0, rows - T}):
+            y, sel, w, z = run(r0, T)
+            assert _same_bits(z, z1[r0:r0 + T]), (T, r0)
+            for i in range(T):
+                a = alone[r0 + i]
+                assert _same_bits(y[i], a[0][0]) and np.array_equal(sel[i], a[1][0]) and _same_bits(w[i], a[2][0])
+    assert int(ws.flags().cpu()[0]) == 0
+
+
 def test_strict_graph_replays(dev):
     """A strict 8-token call (wide prepare, 8-row kernels) captured into a graph: three replays,
     with eager calls of other sizes in between, each bit-identical to the eager call."""
