@@ -94,6 +94,21 @@ def test_exl3_linear(dev, K, rows):
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
 
 
+@pytest.mark.parametrize("shape", [(4096, 128), (7168, 256)])
+@pytest.mark.parametrize("rows", [1, 2, 5])
+def test_exl3_linear_many_splits(dev, shape, rows):
+    """Few output columns and a long input: the decode GEMV's k-split takes every 128-chunk of the
+    input (32 and 56 splits), so the epilogue sums its partials in several batches of 16."""
+    ops = _ops()
+    n_in, n_out = shape
+    rng = np.random.default_rng(n_in + rows)
+    tr, suh, svh = synth.projection(rng, n_in, n_out, 4, svh_scale=1 / np.sqrt(n_in))
+    x = rng.standard_normal((rows, n_in)).astype(np.float16)
+    y = ops.exl3_linear(to_dev(x, dev), to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), 4).cpu().numpy()
+    ref = coop.exl3_linear(x, tr, suh, svh, 4)
+    assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
+
+
 @pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
 @pytest.mark.parametrize("rows", [17, 64, 100])
 def test_exl3_linear_mfma_path(dev, K, rows):
