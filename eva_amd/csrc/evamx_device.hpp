@@ -211,12 +211,76 @@ __device__ __forceinline__ float xor_lane_f(float v, int lane)
     return __builtin_bit_cast(float, xor_lane<M>(__builtin_bit_cast(uint32_t, v), lane));
 }
 
-// Butterfly where the partner lives in lane ^ M; the upper lane (stage bit set) takes a - b.
+// The value of the lane that DPP pattern CTRL selects, as an operand the compiler folds into the
+// add that consumes it (every lane of the patterns used here has a source, so the bound control
+// changes nothing).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+// The row swaps of xor_lane<16> and <32> as a pair (A, B): in the lower block of each pair of
+// blocks (lane & M clear) A is the lane's own value and B its partner's, in the upper block A is
+// the partner's and B its own.
+template <int M>
+__device__ __forceinline__ void swap_pair(float v, float& a, float& b)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        a = __builtin_bit_cast(float, (uint32_t)r[0]);
+        b = __builtin_bit_cast(float, (uint32_t)r[1]);
+    } else {
+        static_assert(M == 32, "row swaps: lane xor 16 or 32");
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        a = __builtin_bit_cast(float, (uint32_t)r[0]);
+        b = __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
+}
+
+// Butterfly where the partner p lives in lane ^ M; the upper lane (stage bit set) takes a - b:
+// v + p in the lower lane, p - v in the upper one, computed as p + (+-v) (the same IEEE sums: a
+// sign flip is exact) so that the DPP lane read folds into the add; for M = 16, 32 as A + (+-B)
+// from the row swap's pair, which is v + p in the lower block and p - v in the upper one.
 template <int M>
 __device__ __forceinline__ float bfly_x(float v, int lane)
 {
-    const float p = xor_lane_f<M>(v, lane);
-    return (lane & M) ? (p - v) : (v + p);
+    if constexpr (M == 16 || M == 32) {
+        float a, b;
+        swap_pair<M>(v, a, b);
+        return a + ((lane & M) ? -b : b);
+    } else {
+        const float sv = (lane & M) ? -v : v;
+        if constexpr (M == 4) {
+            // both rotations in every lane, then a select: a DPP read inside a lane-dependent
+            // branch would run with half the lanes off and read them as zeros
+            const float r4 = dpp_f<0x124>(v) + sv, r12 = dpp_f<0x12C>(v) + sv;             // row_ror:4 / :12
+            return (lane & 4) ? r4 : r12;
+        } else if constexpr (M == 8) {
+            return dpp_f<0x128>(v) + sv;                                                     // row_ror:8
+        } else {
+            return dpp_f<M == 1 ? 0xB1 : 0x4E>(v) + sv;                                      // quad_perm
+        }
+    }
+}
+
+// v + (v of lane ^ M) in every lane, the lane read folded into the add as in bfly_x.
+template <int M>
+__device__ __forceinline__ float pair_sum(float v, int lane)
+{
+    if constexpr (M == 16 || M == 32) {
+        float a, b;
+        swap_pair<M>(v, a, b);
+        return a + b;
+    } else if constexpr (M == 4) {
+        const float r4 = dpp_f<0x124>(v) + v, r12 = dpp_f<0x12C>(v) + v;                   // as in bfly_x
+        return (lane & 4) ? r4 : r12;
+    } else if constexpr (M == 8) {
+        return dpp_f<0x128>(v) + v;
+    } else {
+        return dpp_f<M == 1 ? 0xB1 : 0x4E>(v) + v;
+    }
 }
 
 }  // namespace evamx

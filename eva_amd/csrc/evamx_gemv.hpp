@@ -584,12 +584,12 @@ inline int tmax_for(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4
 __device__ __forceinline__ float wave_sum(float v)
 {
     const int lane = threadIdx.x & 63;
-    v += xor_lane_f<1>(v, lane);
-    v += xor_lane_f<2>(v, lane);
-    v += xor_lane_f<4>(v, lane);
-    v += xor_lane_f<8>(v, lane);
-    v += xor_lane_f<16>(v, lane);
-    v += xor_lane_f<32>(v, lane);
+    v = pair_sum<1>(v, lane);
+    v = pair_sum<2>(v, lane);
+    v = pair_sum<4>(v, lane);
+    v = pair_sum<8>(v, lane);
+    v = pair_sum<16>(v, lane);
+    v = pair_sum<32>(v, lane);
     return v;
 }
 
