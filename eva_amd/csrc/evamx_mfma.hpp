@@ -143,8 +143,8 @@ __device__ __forceinline__ void mfma_row_sums(const GlobalRows& src, const int* 
         const float* sp = src.sums + (size_t)s * src.sums_stride;
         float t = 0.0f;
         for (int c = c0 + g; c < c1; c += 4) t += sp[c];
-        t += xor_lane_f<16>(t, lane);
-        t += xor_lane_f<32>(t, lane);
+        t = pair_sum<16>(t, lane);
+        t = pair_sum<32>(t, lane);
         v[mb] = t;
     }
 #pragma unroll

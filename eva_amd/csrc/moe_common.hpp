@@ -111,14 +111,26 @@ __device__ __forceinline__ uint64_t pack_key(float k, int e)
 
 // Maximum of one 32-bit value per lane over the wave, in every lane: quad maxima by two quad
 // permutations, row maxima by rotations of 4 and 8 within the row, then across rows.
+// The DPP reads are operands the compiler folds into the max (every lane of these patterns has a
+// source); across rows, the row swap's pair holds the lane's own value and its partner's in some
+// order, so their max is the pair's.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v, int lane)
 {
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, false));    // quad_perm [1,0,3,2]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, false));    // quad_perm [2,3,0,1]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xf, 0xf, false));   // row_ror:4
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false));   // row_ror:8
-    v = max(v, xor_lane<16>(v, lane));
-    v = max(v, xor_lane<32>(v, lane));
+    (void)lane;
+    v = max(v, dpp_u<0xB1>(v));                          // quad_perm [1,0,3,2]
+    v = max(v, dpp_u<0x4E>(v));                          // quad_perm [2,3,0,1]
+    v = max(v, dpp_u<0x124>(v));                         // row_ror:4
+    v = max(v, dpp_u<0x128>(v));                         // row_ror:8
+    const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)r16[0], (uint32_t)r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = max((uint32_t)r32[0], (uint32_t)r32[1]);
     return v;
 }
 
