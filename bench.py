@@ -939,9 +939,11 @@ def run_linear(torch, args):
                                f"{copies} resident copies in one graph (BASELINE configs[0])",
                    "in": n_in, "out": n_out, "tokens": T, "bits": bits, "copies": copies},
         "step_bytes": int(nbytes), "frac_hbm_step": round(gbps / PEAK_HBM, 4),
-        "roofline": {"bound": "hbm", "kernel": "exl3_linear (" + ("2 launches: GEMV with its input rotation, epilogue"
-                                                            if T <= 2 else "rotation, GEMV or MFMA tiles, epilogue")
-                     + " per call)", "achieved": round(gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "exl3_linear (" + (
+                         "1 launch: GEMV with its input rotation, the epilogue in each column group's last workgroup"
+                         if T <= 2 else "3 launches: rotation, GEMV, epilogue" if T <= 16
+                         else "2 launches: rotation, MFMA tiles with their epilogue") + " per call)",
+                     "achieved": round(gbps, 1),
                      "peak": PEAK_HBM, "unit": "GB/s", "frac": round(gbps / PEAK_HBM, 4), "traffic": None},
     }
     if not args.no_cpu_baseline:

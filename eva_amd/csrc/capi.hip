@@ -236,6 +236,9 @@ extern "C" int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, 
                   "evamx_exl3_linear: in/out (%d, %d) must be positive multiples of 128", in_features, out_features);
     EVAMX_REQUIRE(gemv_rate(k2), "evamx_exl3_linear: bit rate %g not in {1.5,2,2.5,3,3.5,4,5}", (double)bits);
     const size_t need = linear_workspace(rows, in_features, out_features, nullptr, nullptr);
+    EVAMX_REQUIRE(rows > 16 || need < ((size_t)1 << 31),
+                  "evamx_exl3_linear: %d x %d with %d rows exceeds the decode path's 2 GiB of partials", in_features,
+                  out_features, rows);
     if (workspace_bytes < need) {
         set_error("evamx_exl3_linear: workspace %zu bytes < %zu", workspace_bytes, need);
         return EVAMX_ENOSPACE;

@@ -551,32 +551,6 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
 #undef EVAMX_RUN
 }
 
-// Runtime rate (k2 = 2 x bits) -> instantiated GEMV: 1.5, 2, 2.5, 3, 3.5, 4, 5 bits. An
-// unsupported rate writes zero partials (the caller flags it), so no output reads stale data.
-template <int TMAX>
-__device__ __forceinline__ void gemv_dispatch_k(int k2, const uint32_t* trellis, int nt_n, int cg, int c0, int c1,
-                                                const GlobalRows& src, const int* slot_of, int tm, float* part,
-                                                size_t part_stride)
-{
-    switch (k2) {
-        case 3: gemv_chunk<3, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 4: gemv_chunk<4, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 5: gemv_chunk<5, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 6: gemv_chunk<6, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 7: gemv_chunk<7, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 8: gemv_chunk<8, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        case 10: gemv_chunk<10, TMAX>(trellis, nt_n, cg, c0, c1, src, slot_of, tm, part, part_stride); break;
-        default: {
-            const int lane = threadIdx.x & 63;
-            for (int m = 0; m < tm; ++m) {
-                float* dst = part + (size_t)slot_of[m] * part_stride + cg * 128;
-                dst[lane_col(lane, 0)] = 0.0f;
-                dst[lane_col(lane, 1)] = 0.0f;
-            }
-        }
-    }
-}
-
 // Smallest compiled row bound that covers `rows` rows per chunk (wider chunks loop over it).
 inline int tmax_for(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
 

@@ -3,10 +3,12 @@
 // Reference: ELinear.forward -> LinearEXL3 (runtime/ds41/exl3_linear.py:97-131), kernel
 // exl3_gemv_kernel.cuh:217-234 (input: fp16 x*suh, Hadamard, fp16), 295-459 (GEMV, fp16 C),
 // 463-490 with hadamard_inner.cuh:93-147 (output Hadamard to fp16, fp16 product with svh).
-// Up to 16 rows, two launches: a k-split decode GEMV whose waves rotate their own input chunks
-// (fp16(H128(fp16(x * suh)))) into LDS while their first weight loads are in flight, writing
-// fp32 partials; and the output epilogue (the partials summed in fixed order, fp16 C,
-// Hadamard, fp16 svh product).
+// Up to 2 rows, one launch: a k-split decode GEMV whose waves rotate their own input chunks
+// (fp16(H128(fp16(x * suh)))) into LDS while their first weight loads are in flight, writing fp32
+// partials; the workgroup that arrives last at its column group's counter then runs that group's
+// output epilogue (the partials summed in fixed split order, fp16 C, Hadamard, fp16 svh product).
+// 3 to 16 rows, three launches: the input rotation, the same GEMV on the rotated rows, and the
+// same epilogue in a launch of its own.
 // More rows, two launches: the input rotation, then the MFMA path, one workgroup per (64-row
 // tile, 128 output columns) whose waves take fixed k-ranges, meet in LDS (summed in wave
 // order) and run the output epilogue. In both paths a row's arithmetic depends on in/out only,
@@ -35,7 +37,61 @@ struct LinParams {
     half_t* xr;        // [rows][in]
     float* xsum;       // [rows][in/128]
     float* part;       // [ks][rows][out]
+    unsigned long long* arrive;   // arrival counters of the decode path, one per ARRIVE_STRIDE words
 };
+
+// Partials cross workgroups inside the launch: stored write-through (relaxed device-scope atomic
+// stores) and read by the column group's last workgroup from the memory side (sc1 loads), so
+// neither side needs a cache-wide fence.
+__device__ __forceinline__ void st_partial(float* d, float v)
+{
+    __hip_atomic_store(d, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival counter of a column group: one 64-bit word, high half a tag, low half the arrivals.
+// A word at rest holds (ARRIVE_REST, 0); each of the n workgroups adds 1 and the one whose add
+// brings the count to n is the last, which puts the word back to rest for the next call (graph
+// replays included), so a call needs no clearing launch. A word in any other state (a workspace's
+// first use: its bytes are whatever the memory held) is detected by the add's old value; such an
+// arrival's add is not counted, and it counts itself with compare-and-swap instead, taking the
+// word to (ARRIVE_FIX, 1) or adding 1 to an (ARRIVE_FIX, c) word; later adds onto an ARRIVE_FIX
+// word count as usual. Each arrival is counted exactly once either way, and the swap loop ends
+// since each failed swap means another arrival succeeded. The tags have four distinct bytes, so
+// fill patterns of one repeated byte never pass for a counting word.
+constexpr unsigned ARRIVE_REST = 0x3c6ef372u;
+// Counters sit a cache line (128 bytes) apart: atomics on one line are serialised where they are
+// performed, and column groups arrive at the same time.
+constexpr int ARRIVE_STRIDE = 16;
+constexpr unsigned ARRIVE_FIX = 0xa54ff53au;
+
+__device__ __forceinline__ bool counting(unsigned long long w, unsigned n)
+{
+    const unsigned hi = (unsigned)(w >> 32);
+    return (hi == ARRIVE_REST || hi == ARRIVE_FIX) && (unsigned)w < n;
+}
+
+__device__ bool arrive_last(unsigned long long* word, unsigned n)
+{
+    const unsigned long long old = __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool last;
+    if (counting(old, n)) {
+        last = (unsigned)old + 1 == n;
+    } else {
+        unsigned long long cur = old + 1;       // refreshed by the first failed swap
+        for (;;) {
+            const unsigned long long next = (unsigned)(cur >> 32) == ARRIVE_FIX && (unsigned)cur < n
+                                                ? cur + 1
+                                                : ((unsigned long long)ARRIVE_FIX << 32) | 1ull;
+            if (__hip_atomic_compare_exchange_strong(word, &cur, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)) {
+                last = (unsigned)next == n;
+                break;
+            }
+        }
+    }
+    if (last) __hip_atomic_store(word, (unsigned long long)ARRIVE_REST << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
 
 // Rotated inputs of tm rows (rows r0 .. r0 + tm - 1 of x) over the 128-chunks [w0, w1) into
 // the wave's LDS rows (row m at dst + m * LIN_CW * 64 words, chunk w0 + j at word 64 j), with
@@ -120,8 +176,8 @@ __device__ __forceinline__ void lin_rows(const LinParams& p, int r0, int tm, int
     for (int m = 0; m < TM; ++m) {
         if (m < tm) {
             float* dst = p.part + ((size_t)ks * p.rows + r0 + m) * p.out;
-            dst[col0] = mul1_affine(acc[m][0], xs[m]);
-            dst[col1] = mul1_affine(acc[m][1], xs[m]);
+            st_partial(dst + col0, mul1_affine(acc[m][0], xs[m]));
+            st_partial(dst + col1, mul1_affine(acc[m][1], xs[m]));
         }
     }
 }
@@ -133,34 +189,116 @@ __device__ __forceinline__ void lin_item(const LinParams& p, int cg, int ks, int
     else lin_rows<K2, 2>(p, 0, p.rows, cg, ks, c0, c1, lds);
 }
 
-// One wave per (128 output columns, k-split); each row's reduction order depends only on
-// in/out, never on how many rows share the call. TM (1 or 2) rows: inputs rotated in the wave.
-template <int TM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void lin_gemv_kernel(LinParams p)
+// Partials of 16 splits for the lane's two columns (byte offsets vo and vo + 32 in rs, splits sb
+// bytes apart from split q0 on), the loads all issued before the adds; splits from `valid` on are
+// loaded clamped and not added. The loads read the memory side (sc1), where the other workgroups'
+// write-through stores went; buffer loads take the split offsets in scalar registers, so no
+// vector instruction computes an address.
+constexpr int LD_SC1 = 16;            // buffer load cache policy: device scope (sc1)
+
+template <bool FULL, int POL>
+__device__ __forceinline__ void lin_sum16(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t sb, int q0, int valid,
+                                          float& v0, float& v1)
 {
-    __shared__ uint32_t xl[4][TM * LIN_CW * 64];
-    const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int ncg = p.out / 128;
-    if (wid >= ncg * p.ks) return;
-    const int cg = __builtin_amdgcn_readfirstlane(wid / p.ks), ks = __builtin_amdgcn_readfirstlane(wid % p.ks);
-    const int nch = p.in / 128;
-    const int c0 = nch * ks / p.ks, c1 = nch * (ks + 1) / p.ks;
-    uint32_t* lds = xl[threadIdx.x >> 6];
-    switch (p.k2) {
-        case 3: lin_item<3, TM>(p, cg, ks, c0, c1, lds); break;
-        case 4: lin_item<4, TM>(p, cg, ks, c0, c1, lds); break;
-        case 5: lin_item<5, TM>(p, cg, ks, c0, c1, lds); break;
-        case 6: lin_item<6, TM>(p, cg, ks, c0, c1, lds); break;
-        case 7: lin_item<7, TM>(p, cg, ks, c0, c1, lds); break;
-        case 8: lin_item<8, TM>(p, cg, ks, c0, c1, lds); break;
-        case 10: lin_item<10, TM>(p, cg, ks, c0, c1, lds); break;
-        default: break;                 // the rate is validated on the host
+    float t0[16], t1[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t so = sb * (uint32_t)(q0 + (FULL ? i : min(i, valid - 1)));
+        t0[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, POL));
+        t1[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, vo + 32, so, POL));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (FULL || i < valid) {
+            v0 += t0[i];
+            v1 += t1[i];
+        }
+}
+
+// Output epilogue of row m of a column group: the row's k-split partials summed in split order
+// (one memory round trip per 16 splits), C to fp16, Hadamard, fp16 svh product. POL: LD_SC1 in
+// the launch that wrote the partials (run by the group's last workgroup after its arrival, where
+// every instruction is on the call's critical path), 0 in a launch of its own.
+template <int POL>
+__device__ __forceinline__ void lin_epilogue_row(const LinParams& p, int cg, int m, const float (&sv)[2])
+{
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc((const uint32_t*)p.part);
+    const uint32_t vo = 4u * (uint32_t)(m * p.out + cg * 128 + lane_col(lane, 0));   // column 1: + 32 bytes
+    const uint32_t sb = 4u * (uint32_t)(p.rows * p.out);
+    float v0 = 0.0f, v1 = 0.0f;
+    for (int q0 = 0; q0 < p.ks; q0 += 16) {
+        if (q0 + 16 <= p.ks) lin_sum16<true, POL>(rs, vo, sb, q0, 16, v0, v1);
+        else lin_sum16<false, POL>(rs, vo, sb, q0, p.ks - q0, v0, v1);
+    }
+    v0 = h2f(f2h(v0));                  // C in fp16
+    v1 = h2f(f2h(v1));
+    had128_lane(v0, v1, lane);
+    half_t* y = p.y + (size_t)m * p.out + cg * 128 + lane_col(lane, 0);
+    y[0] = f2h(h2f(f2h(v0)) * sv[0]);
+    y[8] = f2h(h2f(f2h(v1)) * sv[1]);
+}
+
+// After a workgroup's waves stored their partials: wait until every store is acknowledged, arrive
+// at the column group's counter, and run the epilogue if last (the stores of every workgroup of
+// the group then precede the loads). One row: wave 0 arrives and runs the epilogue alone, with no
+// second barrier; two: the arrival is shared through LDS and wave m runs row m.
+template <int TM>
+__device__ __forceinline__ void lin_arrive(const LinParams& p, int cg, int n, const float (&sv)[2])
+{
+    unsigned long long* word = p.arrive + (size_t)cg * ARRIVE_STRIDE;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if constexpr (TM == 1) {
+        if (wave != 0) return;
+        int l = 0;
+        if (threadIdx.x == 0) l = arrive_last(word, (unsigned)n);
+        if (__builtin_amdgcn_readfirstlane(l)) lin_epilogue_row<LD_SC1>(p, cg, 0, sv);
+    } else {
+        __shared__ int last;
+        if (threadIdx.x == 0) last = arrive_last(word, (unsigned)n);
+        __syncthreads();
+        if (last && wave < p.rows) lin_epilogue_row<LD_SC1>(p, cg, wave, sv);
     }
 }
 
+// The lane's two svh values, loaded at the start of the launch (the epilogue needs them only in
+// the last workgroup, but then without waiting for them).
+__device__ __forceinline__ void lin_load_sv(const LinParams& p, int cg, float (&sv)[2])
+{
+    const int lane = threadIdx.x & 63;
+    sv[0] = h2f(p.svh[cg * 128 + lane_col(lane, 0)]);
+    sv[1] = h2f(p.svh[cg * 128 + lane_col(lane, 1)]);
+}
+
+// Decode path: one workgroup of four waves per (128 output columns, quarter q of the k-splits),
+// wave w taking split 4q + w (waves past the last split only arrive); each row's reduction order
+// depends only on in/out, never on how many rows share the call. One kernel per rate (the host
+// picks it). TM (1 or 2) rows: inputs rotated in the wave.
+template <int K2, int TM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void lin_gemv_kernel(LinParams p)
+{
+    __shared__ uint32_t xl[4][TM * LIN_CW * 64];
+    const int nq = (p.ks + 3) >> 2;
+    const int cg = blockIdx.x / nq, q = blockIdx.x % nq;
+    const int ks = __builtin_amdgcn_readfirstlane(4 * q + (threadIdx.x >> 6));
+    float sv[2];
+    lin_load_sv(p, cg, sv);
+    if (ks < p.ks) {
+        const int nch = p.in / 128;
+        const int c0 = nch * ks / p.ks, c1 = nch * (ks + 1) / p.ks;
+        lin_item<K2, TM>(p, cg, ks, c0, c1, xl[threadIdx.x >> 6]);
+    }
+    lin_arrive<TM>(p, cg, nq, sv);
+}
+
 // 3 to LIN_GEMV_ROWS rows: the rows rotated beforehand (lin_rotate_kernel), read through
-// scalar loads (wider row blocks in LDS would not fit the register budget).
-template <int TMAX>
+// scalar loads (wider row blocks in LDS would not fit the register budget); one wave per (128
+// output columns, k-split), the output epilogue in a launch of its own (lin_epilogue_kernel). At
+// these row counts the last workgroup of a column group would run many rows' epilogues one after
+// another (16 rows at 2048 x 7168: 38.6 us per call, against 32.1 us with the epilogue launch).
+template <int K2, int TMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void lin_gemv_rows_kernel(LinParams p)
 {
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
@@ -169,47 +307,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
     const int cg = __builtin_amdgcn_readfirstlane(wid / p.ks), ks = __builtin_amdgcn_readfirstlane(wid % p.ks);
     const int nch = p.in / 128;
     const int c0 = nch * ks / p.ks, c1 = nch * (ks + 1) / p.ks;
-    gemv_dispatch_k<TMAX>(p.k2, p.trellis, p.out / 16, cg, c0, c1, GlobalRows{p.xr, (size_t)p.in, p.xsum, nch},
-                          k_iota64, p.rows, p.part + (size_t)ks * p.rows * p.out, (size_t)p.out);
+    gemv_chunk<K2, TMAX>(p.trellis, p.out / 16, cg, c0, c1, GlobalRows{p.xr, (size_t)p.in, p.xsum, nch}, k_iota64,
+                         p.rows, p.part + (size_t)ks * p.rows * p.out, (size_t)p.out);
 }
 
+// One wave per (row, 128 output columns).
 __global__ __launch_bounds__(256) void lin_epilogue_kernel(LinParams p)
 {
-    const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int ncg = p.out / 128;
     if (wid >= ncg * p.rows) return;
     const int m = wid / ncg, cg = wid % ncg;
-    float sv[2];                                       // loaded with the partials
-#pragma unroll
-    for (int h = 0; h < 2; ++h) sv[h] = h2f(p.svh[cg * 128 + lane_col(lane, h)]);
-    // the k-split partials in fixed order; the loads of up to 16 splits of both columns are issued
-    // before their adds (one memory round trip per 16 splits: the call is latency-bound)
-    float v[2] = {0.0f, 0.0f};
-    const size_t stride = (size_t)p.rows * p.out;
-    const float* pp[2] = {p.part + (size_t)m * p.out + cg * 128 + lane_col(lane, 0),
-                          p.part + (size_t)m * p.out + cg * 128 + lane_col(lane, 1)};
-    for (int q0 = 0; q0 < p.ks; q0 += 16) {
-        float t[2][16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (q0 + i < p.ks)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) t[h][i] = gptr<float>(pp[h])[(q0 + i) * stride];
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (q0 + i < p.ks)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) v[h] += t[h][i];
+    float sv[2];
+    lin_load_sv(p, cg, sv);
+    lin_epilogue_row<0>(p, cg, m, sv);
+}
+
+// Decode path launches of one rate: up to 2 rows one launch (workgroups per (column group, 4
+// splits)); 3 to 16 rows the GEMV (a wave per (column group, split)) and the epilogue.
+template <int K2>
+void launch_gemv_rate(const LinParams& p, hipStream_t stream)
+{
+    const int ncg = p.out / 128;
+    if (p.rows <= LIN_ROT_ROWS) {
+        const dim3 grid((unsigned)(ncg * ((p.ks + 3) / 4)));
+        if (p.rows == 1) hipLaunchKernelGGL((lin_gemv_kernel<K2, 1>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((lin_gemv_kernel<K2, 2>), grid, dim3(256), 0, stream, p);
+        return;
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) v[h] = h2f(f2h(v[h]));    // C in fp16
-    had128_lane(v[0], v[1], lane);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int col = cg * 128 + lane_col(lane, h);
-        p.y[(size_t)m * p.out + col] = f2h(h2f(f2h(v[h])) * sv[h]);
-    }
+    const dim3 grid((unsigned)((ncg * p.ks + 3) / 4));
+    if (p.rows <= 4) hipLaunchKernelGGL((lin_gemv_rows_kernel<K2, 4>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((lin_gemv_rows_kernel<K2, 8>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(lin_epilogue_kernel, dim3((unsigned)((ncg * p.rows + 3) / 4)), dim3(256), 0, stream, p);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -340,16 +469,20 @@ int linear_ksplit(int rows, int in, int out)
     return ks;
 }
 
-// Workspace: up to 2 rows, the fp32 partials [ks][rows][out]; 3 to 16 rows, also the rotated
-// rows [rows][in] fp16 and their 128-chunk sums [rows][in/128]; MFMA path, those two only.
+// Workspace: the column groups' arrival counters (out/128 of them, 128 bytes apart, at offset 0
+// for every row count, so that no other layout overwrites them); from 3 rows the rotated rows
+// [rows][in] fp16 and their 128-chunk sums [rows][in/128]; up to 16 rows the fp32 partials
+// [ks][rows][out].
+static size_t arrive_bytes(int out) { return (size_t)(out / 128) * ARRIVE_STRIDE * 8; }
+
 size_t linear_workspace(int rows, int in, int out, size_t* off_part, size_t* off_sum)
 {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    size_t o = 0;
+    size_t o = al(arrive_bytes(out));
     if (off_sum) *off_sum = 0;
     if (off_part) *off_part = 0;
     if (rows > LIN_ROT_ROWS) {
-        o = al((size_t)rows * in * 2);
+        o = al(o + (size_t)rows * in * 2);
         if (off_sum) *off_sum = o;
         o = al(o + (size_t)rows * (in / 128) * 4);
     }
@@ -373,7 +506,9 @@ int launch_linear(const void* x, int rows, int in, int out, const void* trellis,
     p.suh = (const half_t*)suh;
     p.svh = (const half_t*)svh;
     p.y = (half_t*)y;
-    p.xr = rows > LIN_ROT_ROWS ? (half_t*)ws : nullptr;
+    const size_t off_xr = (arrive_bytes(out) + 255) & ~(size_t)255;
+    p.arrive = (unsigned long long*)ws;
+    p.xr = rows > LIN_ROT_ROWS ? (half_t*)((char*)ws + off_xr) : nullptr;
     p.xsum = rows > LIN_ROT_ROWS ? (float*)((char*)ws + off_sum) : nullptr;
     p.part = rows <= LIN_GEMV_ROWS ? (float*)((char*)ws + off_part) : nullptr;
     if (rows > LIN_ROT_ROWS) {
@@ -385,17 +520,15 @@ int launch_linear(const void* x, int rows, int in, int out, const void* trellis,
         hipLaunchKernelGGL(lin_mfma_kernel, dim3((unsigned)(tiles * (out / 128))), dim3(64 * LM_WAVES), 0, stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    {
-        const int waves = (out / 128) * p.ks;
-        const dim3 grid((waves + 3) / 4);
-        if (rows == 1) hipLaunchKernelGGL(lin_gemv_kernel<1>, grid, dim3(256), 0, stream, p);
-        else if (rows == 2) hipLaunchKernelGGL(lin_gemv_kernel<2>, grid, dim3(256), 0, stream, p);
-        else if (rows <= 4) hipLaunchKernelGGL(lin_gemv_rows_kernel<4>, grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL(lin_gemv_rows_kernel<8>, grid, dim3(256), 0, stream, p);
-    }
-    {
-        const int waves = (out / 128) * rows;
-        hipLaunchKernelGGL(lin_epilogue_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+    switch (k2) {
+        case 3: launch_gemv_rate<3>(p, stream); break;
+        case 4: launch_gemv_rate<4>(p, stream); break;
+        case 5: launch_gemv_rate<5>(p, stream); break;
+        case 6: launch_gemv_rate<6>(p, stream); break;
+        case 7: launch_gemv_rate<7>(p, stream); break;
+        case 8: launch_gemv_rate<8>(p, stream); break;
+        case 10: launch_gemv_rate<10>(p, stream); break;
+        default: return -1;             // the rate is validated by the caller
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

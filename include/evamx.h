@@ -63,7 +63,10 @@ size_t evamx_exl3_linear_workspace_bytes(int rows, int in_features, int out_feat
 /* y[rows][out] = svh * H(W^T H(x * suh)) with the reference's fp16 rounding points.
  * rows in 1..65536 (up to 16 rows a decode GEMV, beyond it MFMA tiles; within each a row's result
  * does not depend on how many rows share the call); in/out multiples of 128; bits in
- * {1.5,2,2.5,3,3.5,4,5}. All pointers device. */
+ * {1.5,2,2.5,3,3.5,4,5}. All pointers device. Up to 2 rows the call is one launch: the
+ * workgroups of each 128-column group meet at an arrival counter kept in the workspace, which may
+ * hold anything before its first use (the call then counts with compare-and-swap) and is left at
+ * rest by every call, graph replays included. Calls that share a workspace must not overlap. */
 int evamx_exl3_linear(const void* x_fp16, int rows, int in_features, int out_features,
                       const void* trellis, const void* suh_fp16, const void* svh_fp16, float bits,
                       void* y_fp16, void* workspace, size_t workspace_bytes, evamx_stream_t stream);

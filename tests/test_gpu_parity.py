@@ -94,11 +94,12 @@ def test_exl3_linear(dev, K, rows):
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
 
 
-@pytest.mark.parametrize("shape", [(4096, 128), (7168, 256)])
+@pytest.mark.parametrize("shape", [(4096, 128), (7168, 256), (768, 128), (1280, 256)])
 @pytest.mark.parametrize("rows", [1, 2, 5])
 def test_exl3_linear_many_splits(dev, shape, rows):
-    """Few output columns and a long input: the decode GEMV's k-split takes every 128-chunk of the
-    input (32 and 56 splits), so the epilogue sums its partials in several batches of 16."""
+    """Few output columns: the decode GEMV's k-split takes every 128-chunk of the input (32, 56, 6
+    and 10 splits), so the epilogue sums its partials in several batches of 16, and with 6 and 10
+    splits the last workgroup of a column group has waves past the last split (they only arrive)."""
     ops = _ops()
     n_in, n_out = shape
     rng = np.random.default_rng(n_in + rows)
@@ -107,6 +108,75 @@ def test_exl3_linear_many_splits(dev, shape, rows):
     y = ops.exl3_linear(to_dev(x, dev), to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), 4).cpu().numpy()
     ref = coop.exl3_linear(x, tr, suh, svh, 4)
     assert rel_err_rows(y.astype(np.float32), ref.astype(np.float32)) < TOL
+
+
+ARRIVE_REST = 0x3C6EF372        # high word of a column group's arrival counter at rest
+
+
+@pytest.mark.parametrize("rows", [1, 2])
+def test_exl3_linear_arrival_counters(dev, rows):
+    """Up to 2 rows the linear is one launch whose column groups meet at arrival counters in the
+    workspace. Whatever the workspace held before (all-ones bytes, zeros, random bytes, another
+    shape's partials and counters), the first call gives the bits of a call on a settled
+    workspace and leaves every counter at rest; so do graph replays of the call."""
+    ops = _ops()
+    n_in, n_out = 2048, 1024
+    rng = np.random.default_rng(700 + rows)
+    tr, suh, svh = synth.projection(rng, n_in, n_out, 4, svh_scale=1 / np.sqrt(n_in))
+    x = rng.standard_normal((rows, n_in)).astype(np.float16)
+    args = (to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), 4)
+    xd = to_dev(x, dev)
+    need = ops.lib().evamx_exl3_linear_workspace_bytes(rows, n_in, n_out)
+    ncg = n_out // 128
+
+    def at_rest(ws):                    # one counter per 128 bytes
+        words = ws[: ncg * 128].view(torch.int64).cpu().numpy().astype(np.uint64)[::16]
+        return bool(np.all(words == np.uint64(ARRIVE_REST << 32)))
+
+    settled = torch.empty(need, dtype=torch.uint8, device=dev)
+    ops.exl3_linear(xd, *args, workspace=settled)
+    y0 = ops.exl3_linear(xd, *args, workspace=settled)
+    torch.cuda.synchronize()
+    assert at_rest(settled)
+    ref = coop.exl3_linear(x, tr, suh, svh, 4)
+    assert rel_err_rows(y0.cpu().numpy().astype(np.float32), ref.astype(np.float32)) < TOL
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows)
+    fills = {
+        "ones": torch.full((need,), 0xFF, dtype=torch.uint8, device=dev),
+        "zeros": torch.zeros(need, dtype=torch.uint8, device=dev),
+        "random": torch.randint(0, 256, (need,), generator=g, dtype=torch.uint8, device=dev),
+    }
+    # another shape's call first: its partials and counters sit where this shape's counters are
+    other = torch.empty(max(need, ops.lib().evamx_exl3_linear_workspace_bytes(1, 512, 7168)), dtype=torch.uint8,
+                        device=dev)
+    rng2 = np.random.default_rng(9)
+    tr2, suh2, svh2 = synth.projection(rng2, 512, 7168, 4)
+    ops.exl3_linear(to_dev(rng2.standard_normal((1, 512)).astype(np.float16), dev), to_dev(tr2, dev),
+                    to_dev(suh2, dev), to_dev(svh2, dev), 4, workspace=other)
+    fills["other shape"] = other
+    for name, ws in fills.items():
+        y = ops.exl3_linear(xd, *args, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0), name
+        assert at_rest(ws), name
+
+    ws = fills["random"]
+    ws.copy_(torch.randint(0, 256, (ws.numel(),), generator=g, dtype=torch.uint8, device=dev))
+    out = torch.empty_like(y0)
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            ops.exl3_linear(xd, *args, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y0)
+        assert at_rest(ws)
 
 
 @pytest.mark.parametrize("K", [2, 3, 4, 5, 1.5, 2.5, 3.5])
