@@ -40,59 +40,6 @@ struct LinParams {
     unsigned long long* arrive;   // arrival counters of the decode path, one per ARRIVE_STRIDE words
 };
 
-// Partials cross workgroups inside the launch: stored write-through (relaxed device-scope atomic
-// stores) and read by the column group's last workgroup from the memory side (sc1 loads), so
-// neither side needs a cache-wide fence.
-__device__ __forceinline__ void st_partial(float* d, float v)
-{
-    __hip_atomic_store(d, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Arrival counter of a column group: one 64-bit word, high half a tag, low half the arrivals.
-// A word at rest holds (ARRIVE_REST, 0); each of the n workgroups adds 1 and the one whose add
-// brings the count to n is the last, which puts the word back to rest for the next call (graph
-// replays included), so a call needs no clearing launch. A word in any other state (a workspace's
-// first use: its bytes are whatever the memory held) is detected by the add's old value; such an
-// arrival's add is not counted, and it counts itself with compare-and-swap instead, taking the
-// word to (ARRIVE_FIX, 1) or adding 1 to an (ARRIVE_FIX, c) word; later adds onto an ARRIVE_FIX
-// word count as usual. Each arrival is counted exactly once either way, and the swap loop ends
-// since each failed swap means another arrival succeeded. The tags have four distinct bytes, so
-// fill patterns of one repeated byte never pass for a counting word.
-constexpr unsigned ARRIVE_REST = 0x3c6ef372u;
-// Counters sit a cache line (128 bytes) apart: atomics on one line are serialised where they are
-// performed, and column groups arrive at the same time.
-constexpr int ARRIVE_STRIDE = 16;
-constexpr unsigned ARRIVE_FIX = 0xa54ff53au;
-
-__device__ __forceinline__ bool counting(unsigned long long w, unsigned n)
-{
-    const unsigned hi = (unsigned)(w >> 32);
-    return (hi == ARRIVE_REST || hi == ARRIVE_FIX) && (unsigned)w < n;
-}
-
-__device__ bool arrive_last(unsigned long long* word, unsigned n)
-{
-    const unsigned long long old = __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bool last;
-    if (counting(old, n)) {
-        last = (unsigned)old + 1 == n;
-    } else {
-        unsigned long long cur = old + 1;       // refreshed by the first failed swap
-        for (;;) {
-            const unsigned long long next = (unsigned)(cur >> 32) == ARRIVE_FIX && (unsigned)cur < n
-                                                ? cur + 1
-                                                : ((unsigned long long)ARRIVE_FIX << 32) | 1ull;
-            if (__hip_atomic_compare_exchange_strong(word, &cur, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT)) {
-                last = (unsigned)next == n;
-                break;
-            }
-        }
-    }
-    if (last) __hip_atomic_store(word, (unsigned long long)ARRIVE_REST << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return last;
-}
-
 // Rotated inputs of tm rows (rows r0 .. r0 + tm - 1 of x) over the 128-chunks [w0, w1) into
 // the wave's LDS rows (row m at dst + m * LIN_CW * 64 words, chunk w0 + j at word 64 j), with
 // each row's chunk sums added in chunk order; the same operations as lin_rotate_kernel, so the
@@ -176,8 +123,8 @@ __device__ __forceinline__ void lin_rows(const LinParams& p, int r0, int tm, int
     for (int m = 0; m < TM; ++m) {
         if (m < tm) {
             float* dst = p.part + ((size_t)ks * p.rows + r0 + m) * p.out;
-            st_partial(dst + col0, mul1_affine(acc[m][0], xs[m]));
-            st_partial(dst + col1, mul1_affine(acc[m][1], xs[m]));
+            store_wt(dst + col0, mul1_affine(acc[m][0], xs[m]));
+            store_wt(dst + col1, mul1_affine(acc[m][1], xs[m]));
         }
     }
 }
@@ -191,10 +138,9 @@ __device__ __forceinline__ void lin_item(const LinParams& p, int cg, int ks, int
 
 // Partials of 16 splits for the lane's two columns (byte offsets vo and vo + 32 in rs, splits sb
 // bytes apart from split q0 on), the loads all issued before the adds; splits from `valid` on are
-// loaded clamped and not added. The loads read the memory side (sc1), where the other workgroups'
-// write-through stores went; buffer loads take the split offsets in scalar registers, so no
-// vector instruction computes an address.
-constexpr int LD_SC1 = 16;            // buffer load cache policy: device scope (sc1)
+// loaded clamped and not added. POL LD_SC1: the loads read the memory side, where the other
+// workgroups' write-through stores went; buffer loads take the split offsets in scalar registers,
+// so no vector instruction computes an address.
 
 template <bool FULL, int POL>
 __device__ __forceinline__ void lin_sum16(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t sb, int q0, int valid,
