@@ -494,6 +494,25 @@ __device__ __forceinline__ void gemv_wave_m4(const uint32_t* __restrict__ trelli
         if (kt + d < kt1) step(kt + d, ring[d]);
 }
 
+// sum of sp[c0], sp[c0 + d], ... below c1, added in that order from 0 (as a sequential loop
+// does), the loads of up to B terms issued before their adds: one memory round trip per B terms
+// instead of one per term (a loop that adds each load before issuing the next waits a full round
+// trip per term).
+template <int B>
+__device__ __forceinline__ float strided_sum(const float* sp, int c0, int c1, int d = 1)
+{
+    float xs = 0.0f;
+    for (int c = c0; c < c1; c += B * d) {
+        float t[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) t[j] = gptr<float>(sp)[c + j * d < c1 ? c + j * d : c];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+            if (c + j * d < c1) xs += t[j];
+    }
+    return xs;
+}
+
 // GEMV for a chunk of tm rows over the 128-element k-chunks [c0, c1) with the smallest
 // template that fits; writes fp32 partials part[slot_of[m] * part_stride + column] =
 // sum_k x_k w_k = 0x1eee * sum_k x_k h_k + 0xc931 * sum_k x_k.
@@ -521,9 +540,7 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* trellis, int nt_n, in
         _Pragma("unroll") for (int m = 0; m < TMV; ++m) {                                       \
             if (m < tr) {                                                                       \
                 const int row = so[m];                                                          \
-                const float* sp = src.sums + (size_t)row * src.sums_stride;                     \
-                float xs = 0.0f;                                                                \
-                for (int c = c0; c < c1; ++c) xs += sp[c];                                      \
+                const float xs = strided_sum<4>(src.sums + (size_t)row * src.sums_stride, c0, c1); \
                 float* dst = part + (size_t)row * part_stride;                                  \
                 dst[col0] = mul1_affine(acc[m][0], xs);                                         \
                 dst[col1] = mul1_affine(acc[m][1], xs);                                         \

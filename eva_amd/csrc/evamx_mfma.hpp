@@ -140,9 +140,7 @@ __device__ __forceinline__ void mfma_row_sums(const GlobalRows& src, const int* 
     for (int mb = 0; mb < MB; ++mb) {
         const int r = m16 + 16 * mb;
         const int s = slot_of[r < rows ? r : 0];
-        const float* sp = src.sums + (size_t)s * src.sums_stride;
-        float t = 0.0f;
-        for (int c = c0 + g; c < c1; c += 4) t += sp[c];
+        float t = strided_sum<8>(src.sums + (size_t)s * src.sums_stride, c0 + g, c1, 4);
         t = pair_sum<16>(t, lane);
         t = pair_sum<32>(t, lane);
         v[mb] = t;

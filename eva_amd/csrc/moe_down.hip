@@ -69,9 +69,7 @@ __device__ __forceinline__ void down_rows(const MoeParams& p, const uint32_t* tr
 #pragma unroll
     for (int m = 0; m < TM; ++m) {
         if (m < tm) {
-            const float* sp = p.actsum + (size_t)so[m] * na;
-            float xs = 0.0f;
-            for (int c = c0; c < c1; ++c) xs += sp[c];      // chunk order, as gemv_chunk
+            const float xs = strided_sum<4>(p.actsum + (size_t)so[m] * na, c0, c1);   // chunk order, as gemv_chunk
             float* dst = part + (size_t)so[m] * p.H;
             dst[col0] = mul1_affine(acc[m / 4][0][m % 4], xs);
             dst[col1] = mul1_affine(acc[m / 4][1][m % 4], xs);
