@@ -26,6 +26,10 @@ __constant__ int k_iota64[64] = {0,  1,  2,  3,  4,  5,  6,  7,  8,  9,  10, 11,
 
 constexpr int LIN_GEMV_ROWS = 16;     // decode GEMV up to this many rows, MFMA tiles beyond
 constexpr int LIN_ROT_ROWS = 2;       // the GEMV rotates its own inputs up to this many rows
+// Weight prefetch depth of the 1-2 row GEMV: its waves stream 8 k-slices each at 2048 x 7168,
+// one wave per SIMD; 3 slices in flight measured best (2: 7.58, 3: 6.84, 4: 6.98,
+// 5: 7.07 us per call; the MoE's longer items keep 4).
+constexpr int LIN_PF = 3;
 
 struct LinParams {
     const half_t* x;
@@ -108,7 +112,7 @@ __device__ __forceinline__ void lin_rows(const LinParams& p, int r0, int tm, int
         LinRot<TM> stage{p, tm, w0, w1, lane, {}, srs, lds, xs};
 #pragma unroll
         for (int m = 0; m < TM; ++m) stage.xrs[m] = xrs[m];
-        gemv_wave<K2, TM>(p.trellis, p.out / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+        gemv_wave<K2, TM, LIN_PF>(p.trellis, p.out / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
     };
     if (c1 - c0 <= LIN_CW) {
         window(c0, c1);
