@@ -8,6 +8,10 @@ namespace evamx {
 
 constexpr int DOWN_CW = 4;                         // 128-chunks of activations per LDS window
 constexpr int DOWN_RW = DOWN_CW * 64 + 8;          // words of an LDS row (padded: a quad's rows in distinct banks)
+// Weight slices in flight per wave: the down items are short (32 k-slices at one token), and 3
+// measured faster than 4 (one token 61.2-61.9 against 62.0-63.3 us, 16 strict tokens 422-431
+// against 429-439 us, alternating runs on one box; 6 was slower).
+constexpr int DOWN_PF = 3;
 
 // The rows so[0..tm) of act over the 128-chunks [w0, w1) into LDS (row m at dst + m * DOWN_RW,
 // chunk w0 + j at word 64 j): issue() loads them (chunks past the window reload its last one, in
@@ -63,7 +67,7 @@ __device__ __forceinline__ void down_rows(const MoeParams& p, const uint32_t* tr
         for (int m = 0; m < TM; ++m) stage.rs[m] = rs[m];
         XLds4<NG> src;
         src.init(lds, DOWN_RW, 8 * w0, tm);
-        gemv_wave_m4<K2, NG>(trellis, p.H / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+        gemv_wave_m4<K2, NG, DOWN_PF>(trellis, p.H / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
     }
     const int col0 = cg * 128 + lane_col(lane, 0), col1 = cg * 128 + lane_col(lane, 1);
 #pragma unroll
