@@ -10,7 +10,8 @@ constexpr int DOWN_CW = 4;                         // 128-chunks of activations 
 constexpr int DOWN_RW = DOWN_CW * 64 + 8;          // words of an LDS row (padded: a quad's rows in distinct banks)
 // Weight slices in flight per wave: the down items are short (32 k-slices at one token), and 3
 // measured faster than 4 (one token 61.2-61.9 against 62.0-63.3 us, 16 strict tokens 422-431
-// against 429-439 us, alternating runs on one box; 6 was slower).
+// against 429-439 us, alternating runs on one box) and than 2 (down 17.6-18.3 against
+// 20.5-21.0 us at one token) or 6.
 constexpr int DOWN_PF = 3;
 
 // The rows so[0..tm) of act over the 128-chunks [w0, w1) into LDS (row m at dst + m * DOWN_RW,
