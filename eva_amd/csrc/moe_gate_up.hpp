@@ -464,13 +464,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     }
     int e = -1;                                   // the shared expert's unit (u == topk)
     if (u < p.topk) {
-        int id;
-        half_t rw;
-        float w32;
-        slot_routes1(p, lane, id, rw, w32);
-        id = __builtin_amdgcn_readlane(id, u);
-        const half_t rwu = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_readlane((int)__builtin_bit_cast(uint16_t, rw), u));
-        e = __builtin_amdgcn_readfirstlane(slot_local(p, id, rwu, false));
+        auto route = [&]() {
+            int id;
+            half_t rw;
+            float w32;
+            slot_routes1(p, lane, id, rw, w32);
+            id = __builtin_amdgcn_readlane(id, u);
+            const half_t rwu = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_readlane((int)__builtin_bit_cast(uint16_t, rw), u));
+            return __builtin_amdgcn_readfirstlane(slot_local(p, id, rwu, false));
+        };
+        if constexpr (GROUP) {
+            // the workgroup's four waves share the slot: one routes, the others wait for it
+            __shared__ int e_sh;
+            if (wave == 0) {
+                const int e0 = route();
+                if (lane == 0) e_sh = e0;
+            }
+            __syncthreads();
+            e = __builtin_amdgcn_readfirstlane(e_sh);
+        } else {
+            e = route();
+        }
         if (e < 0) return;                        // inactive slot: no partials are read
     }
     const int k2 = __builtin_amdgcn_readfirstlane(k2_gu_of(p, e));
