@@ -301,9 +301,11 @@ constexpr int LD_SC1 = 16;            // buffer load cache policy: device scope 
 // the last, which puts the word back to rest for the next call (graph replays included), so a
 // call needs no clearing launch. A word in any other state (a workspace's first use: its bytes
 // are whatever the memory held) is detected by the add's old value; such an arrival's add is not
-// counted, and it counts itself with compare-and-swap instead, taking the word to (ARRIVE_FIX, 1)
-// or adding 1 to an (ARRIVE_FIX, c) word; later adds onto an ARRIVE_FIX word count as usual. Each
-// arrival is counted exactly once either way, and the swap loop ends since each failed swap means
+// counted, and it counts itself with compare-and-swap instead, adding 1 to a counting word (an
+// (ARRIVE_FIX, c) word, or an (ARRIVE_REST, c) word that the garbage's adds carried into) or
+// taking any other word to (ARRIVE_FIX, 1); later adds onto a counting word count as usual. Each
+// arrival is counted exactly once either way (tests/test_arrive_protocol.py runs the protocol over
+// random interleavings and initial words), and the swap loop ends since each failed swap means
 // another arrival succeeded. The tags have four distinct bytes, so fill patterns of one repeated
 // byte never pass for a counting word. Device-scope adds on one word cost about 12 ns each when
 // they queue (504 workgroups on one word: 7.4 us against 1.7 us spread out), nothing measurable
@@ -328,9 +330,9 @@ __device__ __forceinline__ bool arrive_last(unsigned long long* word, unsigned n
     } else {
         unsigned long long cur = old + 1;       // refreshed by the first failed swap
         for (;;) {
-            const unsigned long long next = (unsigned)(cur >> 32) == ARRIVE_FIX && (unsigned)cur < n
-                                                ? cur + 1
-                                                : ((unsigned long long)ARRIVE_FIX << 32) | 1ull;
+            // a counting word (of either tag) counts the arrivals made since it became one: add
+            // this one; anything else (garbage) restarts the count at this arrival
+            const unsigned long long next = arrive_counting(cur, n) ? cur + 1 : ((unsigned long long)ARRIVE_FIX << 32) | 1ull;
             if (__hip_atomic_compare_exchange_strong(word, &cur, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT)) {
                 last = (unsigned)next == n;
