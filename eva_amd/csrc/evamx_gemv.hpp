@@ -10,6 +10,8 @@
 #pragma once
 #include "evamx_device.hpp"
 
+#include <type_traits>
+
 namespace evamx {
 
 __device__ __forceinline__ float h2f(half_t h) { return (float)h; }
@@ -434,7 +436,8 @@ __device__ __forceinline__ half4_t m4_a(const uint32_t (&a)[8], int kg)
 }
 
 // acc[g][c][i] += sum_k X[4g + i][k] * h_k over the wave's k-range [kt0, kt1) for the lane's column
-// c; groups g with 4g >= tm are skipped. Same ring, decode and prologue protocol as gemv_wave.
+// c, for tm >= 1 rows; groups g with 4g >= tm are skipped. Same ring, decode and prologue protocol
+// as gemv_wave.
 template <int K2, int NG, int PF = 4, typename Pro>
 __device__ __forceinline__ void gemv_wave_m4(const uint32_t* __restrict__ trellis, int nt_n, int cg, int kt0, int kt1,
                                              const XLds4<NG>& xs, int tm, f32x4v_t (&acc)[NG][2], Pro& prologue)
@@ -459,39 +462,50 @@ __device__ __forceinline__ void gemv_wave_m4(const uint32_t* __restrict__ trelli
     if constexpr (Pro::kWork) __builtin_amdgcn_sched_barrier(0);
     prologue.finish();
 
-    // a step reads its slice's activations from LDS first: the decode hides their latency
-    auto step = [&](int kt, LaneWords<K>& w) {
-        uint32_t xa[NG][8];
+    // The loop over the k-slices for NA active groups (the groups holding rows), with no branch
+    // inside a step: a per-group test in the step splits it into blocks that serialise the
+    // decode and the products.
+    auto run = [&](auto na) {
+        constexpr int NA = decltype(na)::value;
+        // a step reads its slice's activations from LDS first: the decode hides their latency
+        auto step = [&](int kt, LaneWords<K>& w) {
+            uint32_t xa[NA][8];
 #pragma unroll
-        for (int g = 0; g < NG; ++g)
-            if (4 * g < tm) xs.load(g, kt, xa[g]);
-        half2_t wp[16];
-        decode_slice<K2>(w, sh, wp);
-        load_slice<K>(w, rsrc, cbase + (uint32_t)min(kt + PF, last) * slice, lane_off, prev_off);
+            for (int g = 0; g < NA; ++g) xs.load(g, kt, xa[g]);
+            half2_t wp[16];
+            decode_slice<K2>(w, sh, wp);
+            load_slice<K>(w, rsrc, cbase + (uint32_t)min(kt + PF, last) * slice, lane_off, prev_off);
 #pragma unroll
-        for (int kg = 0; kg < 4; ++kg)
+            for (int kg = 0; kg < 4; ++kg)
 #pragma unroll
-            for (int g = 0; g < NG; ++g)
-                if (4 * g < tm) {
+                for (int g = 0; g < NA; ++g) {
                     const half4_t a = m4_a(xa[g], kg);
 #pragma unroll
                     for (int c = 0; c < 2; ++c)
                         acc[g][c] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, m4_b(wp, c, kg), acc[g][c], 0, 0, 0);
                 }
-        __builtin_amdgcn_sched_barrier(0);
-    };
+            __builtin_amdgcn_sched_barrier(0);
+        };
 
-    const int n_kt = kt1 - kt0;
-    int kt = kt0;
-    for (; kt + PF <= kt1; kt += PF) {
-        progress_priority(kt - kt0, n_kt);
+        const int n_kt = kt1 - kt0;
+        int kt = kt0;
+        for (; kt + PF <= kt1; kt += PF) {
+            progress_priority(kt - kt0, n_kt);
 #pragma unroll
-        for (int d = 0; d < PF; ++d) step(kt + d, ring[d]);
+            for (int d = 0; d < PF; ++d) step(kt + d, ring[d]);
+        }
+        progress_priority(n_kt, n_kt);
+#pragma unroll
+        for (int d = 0; d < PF - 1; ++d)
+            if (kt + d < kt1) step(kt + d, ring[d]);
+    };
+    static_assert(NG == 1 || NG == 2, "decode path row groups: 1 or 2");
+    if constexpr (NG == 1) {
+        run(std::integral_constant<int, 1>{});
+    } else {
+        if (tm > 4) run(std::integral_constant<int, 2>{});
+        else run(std::integral_constant<int, 1>{});
     }
-    progress_priority(n_kt, n_kt);
-#pragma unroll
-    for (int d = 0; d < PF - 1; ++d)
-        if (kt + d < kt1) step(kt + d, ring[d]);
 }
 
 // sum of sp[c0], sp[c0 + d], ... below c1, added in that order from 0 (as a sequential loop

@@ -182,7 +182,10 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
         XLds4<NG> src;
         src.init(lds, RW, 8 * w0, tm);
         if constexpr (GROUP) {
-            RotStageGroup<TM, NW> stage{p, so, tm, w0, w1, RW, lane, (int)(threadIdx.x >> 6), srs, {}, lds, lsums, xs};
+            // the wave index made provably uniform: the chunk offsets of the staging loads are then scalar
+            // (a per-lane offset puts every load in a loop over the distinct offsets)
+            const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+            RotStageGroup<TM, NW> stage{p, so, tm, w0, w1, RW, lane, wave, srs, {}, lds, lsums, xs};
 #pragma unroll
             for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
             gemv_wave_m4<K2, NG>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
