@@ -499,12 +499,15 @@ __device__ __forceinline__ void gemv_wave_m4(const uint32_t* __restrict__ trelli
         for (int d = 0; d < PF - 1; ++d)
             if (kt + d < kt1) step(kt + d, ring[d]);
     };
-    static_assert(NG == 1 || NG == 2, "decode path row groups: 1 or 2");
+    static_assert(NG == 1 || NG == 2 || NG == 4, "decode path row groups: 1, 2 or 4");
     if constexpr (NG == 1) {
         run(std::integral_constant<int, 1>{});
-    } else {
+    } else if constexpr (NG == 2) {
         if (tm > 4) run(std::integral_constant<int, 2>{});
         else run(std::integral_constant<int, 1>{});
+    } else {
+        // four groups: 9 to 16 rows (9-12 rows too: the fourth group's products are dropped)
+        run(std::integral_constant<int, 4>{});
     }
 }
 

@@ -1,5 +1,6 @@
 // Gate/up launches of the decode path. This unit holds the one-row launch (routing inside it);
-// the multi-row kernels sit in translation units of their own (moe_gate_up2.hip, moe_gate_up8.hip)
+// the multi-row kernels sit in translation units of their own (moe_gate_up2.hip, moe_gate_up8.hip,
+// moe_gate_up16.hip)
 // so that their instantiations compile in parallel.
 #include "moe_gate_up.hpp"
 
@@ -17,7 +18,9 @@ void launch_gate_up_decode(const MoeParams& p, int tmax, hipStream_t stream, hip
         const dim3 grid1(grid.x + 1);
         if (group) launch_timed(moe_gate_up_route1_kernel<true>, grid1, dim3(256), stream, start, stop, p);
         else launch_timed(moe_gate_up_route1_kernel<false>, grid1, dim3(256), stream, start, stop, p);
-    } else if (tmax == 8 && group) {
+    } else if (tmax == 16 && group) {
+        launch_gate_up_decode16(p, grid, stream, start, stop);
+    } else if (tmax >= 8 && group) {
         launch_gate_up_decode8(p, grid, stream, start, stop);
     } else {
         launch_gate_up_decode4(p, group, grid, stream, start, stop);

@@ -1,7 +1,7 @@
 // Gate/up GEMV kernels of the decode path (calls of 1-2 rows, and strict calls): each wave
 // rotates its own inputs into LDS and streams its weights, the products on the matrix cores
 // (moe_gate_up.hip instantiates the one-row kernel, moe_gate_up2.hip the 2- and 4-row ones,
-// moe_gate_up8.hip the 8-row one).
+// moe_gate_up8.hip the 8-row one, moe_gate_up16.hip the one of paired 8-row chunks).
 #pragma once
 #include "moe_common.hpp"
 
@@ -87,21 +87,23 @@ struct RotStage {
 
 // The same rotations shared by the four waves of a workgroup, which then stream four column
 // groups of the same (unit, projection, k-split): wave w rotates chunks w, w + 4, ... of the
-// window into the workgroup's LDS rows and stores each chunk's sum; after a barrier every wave
-// adds the sums in chunk order (the order of the per-wave stage, so the results are the same).
+// window (CW chunks at most) into the workgroup's LDS rows and stores each chunk's sum. After a
+// barrier the rows are ready; add_sums() adds a row's chunk sums in chunk order (the order of the
+// per-wave stage, so the results are the same), after the GEMV so that the sums hold no
+// registers during it. The rows' x words load through one resource with per-row scalar offsets.
 constexpr int ROT_WAVES = 4;
 
-template <int TM, int NW = ROT_WAVES>
+template <int TM, int NW = ROT_WAVES, int CW = ROT_CW>
 struct RotStageGroup {
     static constexpr bool kWork = true;
-    static constexpr int NJ = ROT_CW / NW;            // chunks per wave and window
+    static constexpr int NJ = CW / NW;                 // chunks per wave and window
     const MoeParams& p;
     const int (&so)[TM];
     int tm, w0, w1, row_words, lane, wave;
-    __amdgpu_buffer_rsrc_t suh_rsrc, x_rsrc[TM];
+    __amdgpu_buffer_rsrc_t suh_rsrc, x_rsrc;           // suh of the projection; x from row 0
+    const uint32_t (&xoff)[TM];                         // byte offset of each row's x
     uint32_t* dst;                                      // LDS rows
-    float* sums;                                        // LDS [TM][ROT_CW] chunk sums
-    float (&xs)[TM];
+    float* sums;                                        // LDS [TM][CW] chunk sums
     uint32_t xv[TM][NJ], sv[NJ];
 
     __device__ __forceinline__ int chunk(int i) const { return min(w0 + wave + NW * i, w1 - 1); }
@@ -112,7 +114,8 @@ struct RotStageGroup {
 #pragma unroll
         for (int m = 0; m < TM; ++m)
 #pragma unroll
-            for (int i = 0; i < NJ; ++i) xv[m][i] = __builtin_amdgcn_raw_buffer_load_b32(x_rsrc[m], 4 * lane, 256 * chunk(i), 0);
+            for (int i = 0; i < NJ; ++i)
+                xv[m][i] = __builtin_amdgcn_raw_buffer_load_b32(x_rsrc, 4 * lane, xoff[m] + 256 * chunk(i), 0);
     }
     __device__ __forceinline__ void finish()
     {
@@ -136,26 +139,43 @@ struct RotStageGroup {
                     const half2_t r = {f2h(v0), f2h(v1)};
                     dst[m * row_words + (c - w0) * 64 + lane] = __builtin_bit_cast(uint32_t, r);
                     const float sm = wave_sum(h2f(r.x) + h2f(r.y));
-                    if (lane == 0) sums[m * ROT_CW + (c - w0)] = sm;
+                    if (lane == 0) sums[m * CW + (c - w0)] = sm;
                 }
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int m = 0; m < TM; ++m)
-            if (m < tm)
-                for (int c = 0; c < w1 - w0; ++c) xs[m] += sums[m * ROT_CW + c];
     }
 };
 
-// Words of an LDS row of rotated inputs: ROT_CW chunks, padded so that the four rows a lane quad
+template <int TM, int CW>
+__device__ __forceinline__ void add_sums(const float* sums, int tm, int nc, float (&xs)[TM])
+{
+#pragma unroll
+    for (int m = 0; m < TM; ++m)
+        if (m < tm)
+            for (int c = 0; c < nc; ++c) xs[m] += sums[m * CW + c];
+}
+
+// Chunks of rotated input per LDS window and row of a kernel whose passes take up to TM rows:
+// ROT_CW, and 8 for 16-row passes (a strict call's k-splits span 8 chunks at the DSv3 shape), so
+// that 16 rows take the LDS of 8 rows of ROT_CW chunks.
+template <int TM>
+constexpr int rot_cw() { return TM > 8 ? 8 : ROT_CW; }
+
+// Weight slices in flight per wave in 16-row passes (the four row groups' accumulators and
+// activations leave fewer registers for the ring).
+constexpr int PAIR_PF = 3;
+
+// Words of an LDS row of rotated inputs: CW chunks, padded so that the four rows a lane quad
 // reads start in different banks.
-constexpr int ROT_ROW_WORDS = ROT_CW * 64 + 8;
+template <int CW>
+constexpr int rot_row_words() { return CW * 64 + 8; }
+constexpr int ROT_ROW_WORDS = rot_row_words<ROT_CW>();
 
 // Gate/up GEMV of tm rows (slots slot[0..tm)) over the 128-chunks [c0, c1): each window of at
-// most ROT_CW chunks is rotated into LDS (GROUP: by the workgroup's four waves together), then
-// streamed with the products on the matrix cores (gemv_wave_m4, rows in groups of four); writes
-// the fp32 partials of the rows.
+// most rot_cw<TM>() chunks is rotated into LDS (GROUP: by the workgroup's four waves together),
+// then streamed with the products on the matrix cores (gemv_wave_m4, rows in groups of four);
+// writes the fp32 partials of the rows.
 template <int K2, int TM, bool GROUP, int NW = ROT_WAVES>
 __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                  const int (&so)[TM], int tm, int cg, int c0, int c1, float* part,
@@ -163,44 +183,48 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
 {
     const int lane = threadIdx.x & 63;
     constexpr int NG = (TM + 3) / 4;
+    constexpr int CW = rot_cw<TM>();
     f32x4v_t acc[NG][2];
     float xs[TM];
 #pragma unroll
     for (int g = 0; g < NG; ++g) acc[g][0] = acc[g][1] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int m = 0; m < TM; ++m) xs[m] = 0.0f;
-    constexpr int RW = ROT_ROW_WORDS;
+    constexpr int RW = rot_row_words<CW>();
     const int slots = p.T * p.topk;
-    __amdgpu_buffer_rsrc_t xrs[TM];
-#pragma unroll
-    for (int m = 0; m < TM; ++m) {
-        const int row = so[m] >= slots ? so[m] - slots : so[m] / p.topk;
-        xrs[m] = weight_rsrc((const uint32_t*)((const uint16_t*)p.x + (size_t)row * p.x_stride));
-    }
     const __amdgpu_buffer_rsrc_t srs = weight_rsrc((const uint32_t*)suh);
-    auto window = [&](int w0, int w1) {
+    auto window = [&](int w0, int w1) __attribute__((always_inline)) {
         XLds4<NG> src;
         src.init(lds, RW, 8 * w0, tm);
         if constexpr (GROUP) {
             // the wave index made provably uniform: the chunk offsets of the staging loads are then scalar
             // (a per-lane offset puts every load in a loop over the distinct offsets)
             const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-            RotStageGroup<TM, NW> stage{p, so, tm, w0, w1, RW, lane, wave, srs, {}, lds, lsums, xs};
+            uint32_t xoff[TM];
 #pragma unroll
-            for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
-            gemv_wave_m4<K2, NG>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+            for (int m = 0; m < TM; ++m) {
+                const int row = so[m] >= slots ? so[m] - slots : so[m] / p.topk;
+                xoff[m] = __builtin_amdgcn_readfirstlane((uint32_t)row * (uint32_t)p.x_stride * 2u);
+            }
+            RotStageGroup<TM, NW, CW> stage{p, so, tm, w0, w1, RW, lane, wave, srs, weight_rsrc((const uint32_t*)p.x), xoff,
+                                            lds, lsums, {}, {}};
+            gemv_wave_m4<K2, NG, NG == 4 ? PAIR_PF : 4>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
+            add_sums<TM, CW>(lsums, tm, w1 - w0, xs);
         } else {
             RotStage<TM> stage{p, so, tm, w0, w1, RW, lane, srs, {}, lds, xs};
 #pragma unroll
-            for (int m = 0; m < TM; ++m) stage.x_rsrc[m] = xrs[m];
+            for (int m = 0; m < TM; ++m) {
+                const int row = so[m] >= slots ? so[m] - slots : so[m] / p.topk;
+                stage.x_rsrc[m] = weight_rsrc((const uint32_t*)((const uint16_t*)p.x + (size_t)row * p.x_stride));
+            }
             gemv_wave_m4<K2, NG>(trellis, p.I / 16, cg, 8 * w0, 8 * w1, src, tm, acc, stage);
         }
     };
-    if (c1 - c0 <= ROT_CW) {
+    if (c1 - c0 <= CW) {
         window(c0, c1);                 // the common case, straight-line
     } else {
-        for (int w0 = c0; w0 < c1; w0 += ROT_CW) {
-            window(w0, min(c1, w0 + ROT_CW));
+        for (int w0 = c0; w0 < c1; w0 += CW) {
+            window(w0, min(c1, w0 + CW));
             // this window's reads before the next window's writes
             if constexpr (GROUP) __syncthreads();
             else wave_lds_fence();
@@ -226,7 +250,7 @@ __device__ __forceinline__ void gate_up_rot_fit(const MoeParams& p, const uint32
                                                 const int* slot, int tm, int cg, int c0, int c1, float* part,
                                                 uint32_t* lds, float* lsums)
 {
-    static_assert(TMAX == 1 || TMAX == 2 || TMAX == 4 || TMAX == 8, "decode path rows: 1, 2, 4 or 8 per pass");
+    static_assert(TMAX == 1 || TMAX == 2 || TMAX == 4 || TMAX == 8, "decode path rows: 1, 2, 4 or 8 per unit pass");
     int so[TMAX];
     record_slots<TMAX>(slot, tm, so);
     gate_up_rot_rows<K2, TMAX, GROUP>(p, trellis, suh, so, tm, cg, c0, c1, part, lds, lsums);
@@ -253,11 +277,34 @@ __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint3
 // of 4): the items run column group fastest, so the four waves of a workgroup share unit,
 // projection and k-split (and exit together) and rotate their inputs together; otherwise every
 // wave rotates its own.
+// Paired units (TMAX 16, strict calls): a unit whose record says pair > 0 takes its own rows and
+// the next unit's (two chunks of one expert, at most 16 rows) in one pass, so the expert's weights
+// are decoded once for both; the next unit's waves exit. Every row's arithmetic is that of a pass
+// of its own chunk.
+template <int K2, bool GROUP>
+__device__ __forceinline__ void gate_up_rot_pair(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
+                                                 const UnitRec* rp, int rows, int rows_b, int cg, int c0, int c1,
+                                                 float* part, uint32_t* lds, float* lsums)
+{
+    if (rows_b == 0) {
+        // a unit alone: the 8-row kernel's pass
+        int so[8];
+        record_slots<8>(rp->slot, rows, so);
+        gate_up_rot_rows<K2, 8, GROUP>(p, trellis, suh, so, rows, cg, c0, c1, part, lds, lsums);
+        return;
+    }
+    int so[16];                                   // the first unit is a full chunk
+    record_slots<8>(rp->slot, 8, *(int(*)[8])so);
+    record_slots<8>(rp[1].slot, rows_b, *(int(*)[8])(so + 8));
+    gate_up_rot_rows<K2, 16, GROUP>(p, trellis, suh, so, 8 + rows_b, cg, c0, c1, part, lds, lsums);
+}
+
 template <int TMAX, bool GROUP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_rot_kernel(MoeParams p)
 {
-    __shared__ uint32_t xl[GROUP ? 1 : 4][TMAX * ROT_ROW_WORDS];
-    __shared__ float xsums[TMAX * ROT_CW];
+    static_assert(TMAX != 16 || GROUP, "paired units run with the workgroup's shared rows");
+    __shared__ uint32_t xl[GROUP ? 1 : 4][TMAX * rot_row_words<rot_cw<TMAX>()>()];
+    __shared__ float xsums[TMAX * rot_cw<TMAX>()];
     const int wave = threadIdx.x >> 6;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int ncg = p.I / 128;
@@ -285,6 +332,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
         ks = __builtin_amdgcn_readfirstlane(rem % S);
     }
     const int rows = __builtin_amdgcn_readfirstlane(rp->rows);
+    int rows_b = 0;                             // rows of the paired next unit
+    if constexpr (TMAX == 16) {
+        const int pair = __builtin_amdgcn_readfirstlane(rp->pair);
+        if (pair < 0) return;                   // the previous unit's waves take these rows
+        if (pair > 0) rows_b = __builtin_amdgcn_readfirstlane(rp[1].rows);
+    }
     const int k2 = __builtin_amdgcn_readfirstlane(rp->k2);
     const int nch = p.H / 128;
     const int c0 = nch * ks / S, c1 = nch * (ks + 1) / S;
@@ -293,21 +346,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
     float* part = p.part_gu + ((size_t)ks * 2 + proj) * moe_nslot(p) * p.I;
     uint32_t* lds = xl[GROUP ? 0 : wave];
     switch (k2) {
-        case 3: gate_up_rot_item<3, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
-        case 4: gate_up_rot_item<4, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
-        case 5: gate_up_rot_item<5, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
-        case 6: gate_up_rot_item<6, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
-        case 7: gate_up_rot_item<7, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
-        case 8: gate_up_rot_item<8, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
-        case 10: gate_up_rot_item<10, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); break;
+#define EVAMX_GUX(K2V)                                                                                       \
+        case K2V:                                                                                            \
+            if constexpr (TMAX == 16)                                                                        \
+                gate_up_rot_pair<K2V, GROUP>(p, trellis, suh, rp, rows, rows_b, cg, c0, c1, part, lds, xsums); \
+            else                                                                                             \
+                gate_up_rot_item<K2V, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); \
+            break;
+        EVAMX_GUX(3) EVAMX_GUX(4) EVAMX_GUX(5) EVAMX_GUX(6) EVAMX_GUX(7) EVAMX_GUX(8) EVAMX_GUX(10)
+#undef EVAMX_GUX
         default: {
             // unsupported rate (flagged by the prepare): zero partials, so no output reads stale data
             const int lane = threadIdx.x & 63;
-            for (int m = 0; m < rows; ++m) {
-                float* dst = part + (size_t)rp->slot[m] * p.I + cg * 128;
-                dst[lane_col(lane, 0)] = 0.0f;
-                dst[lane_col(lane, 1)] = 0.0f;
-            }
+            for (int h = 0; h < (rows_b > 0 ? 2 : 1); ++h)
+                for (int m = 0; m < (h ? rows_b : rows); ++m) {
+                    float* dst = part + (size_t)rp[h].slot[m] * p.I + cg * 128;
+                    dst[lane_col(lane, 0)] = 0.0f;
+                    dst[lane_col(lane, 1)] = 0.0f;
+                }
         }
     }
 }

@@ -1,0 +1,13 @@
+// Gate/up launch of the decode path for strict calls of more than 8 rows: an expert's chunks
+// paired, up to 16 rows per pass (the column groups a multiple of ROT_WAVES), in a translation
+// unit of its own so that its instantiations compile in parallel with the others.
+#include "moe_gate_up.hpp"
+
+namespace evamx {
+
+void launch_gate_up_decode16(const MoeParams& p, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
+{
+    launch_timed(moe_gate_up_rot_kernel<16, true>, grid, dim3(256), stream, start, stop, p);
+}
+
+}  // namespace evamx

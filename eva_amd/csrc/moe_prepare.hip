@@ -216,7 +216,7 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
             r.s_gu = ks_of_chunk(kgu, m);
             r.s_d = ks_of_chunk(kd, m);
             r.k2_d = k2d;
-            r.pad0 = 0;
+            r.pair = 0;
 #pragma unroll
             for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = j < rows ? slot_run[j] : slot_run[0];
             r.tr[0] = sh.tbl[EVAMX_TBL_G_TRELLIS][ge];
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(64 * GEMV_PREP_WAVES) void moe_prepare_gemv_kernel(
             r.s_gu = ks_of_chunk(kgu, 1);
             r.s_d = ks_of_chunk(kd, 1);
             r.k2_d = p.k2_shared_d;
-            r.pad0 = 0;
+            r.pair = 0;
 #pragma unroll
             for (int j = 0; j < EVAMX_CHUNK; ++j) r.slot[j] = slots + (j < p.T ? j : 0);
             r.tr[0] = (uint64_t)p.sh_ptr[EVAMX_TBL_G_TRELLIS];
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
             r.s_gu = q.s_gu;
             r.s_d = q.s_d;
             r.k2_d = k2d;
-            r.pad0 = 0;
+            r.pair = pair_units(p) ? unit_pair(c, (ex.cnt[e] + EVAMX_CHUNK - 1) / EVAMX_CHUNK) : 0;
 #pragma unroll
             for (int i = 0; i < EVAMX_CHUNK; ++i) r.slot[i] = sh.order[pos + (i < rows ? i : 0)];
             r.tr[0] = sh.tbl[EVAMX_TBL_G_TRELLIS][e];
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
             r.s_gu = ks_of_chunk(kgu, m);
             r.s_d = ks_of_chunk(kd, m);
             r.k2_d = p.k2_shared_d;
-            r.pad0 = 0;
+            r.pair = pair_units(p) ? unit_pair(c, nsc) : 0;
 #pragma unroll
             for (int i = 0; i < EVAMX_CHUNK; ++i) r.slot[i] = slots + c * EVAMX_CHUNK + (i < rows ? i : 0);
             r.tr[0] = (uint64_t)p.sh_ptr[EVAMX_TBL_G_TRELLIS];
