@@ -249,8 +249,8 @@ void launch_prepare(const MoeParams& p, hipStream_t stream, hipEvent_t start, hi
 // routes inside), 2 chunks in passes of up to 4 rows, 8 up to 8 rows per pass (gate/up falls back
 // to 2-row passes when the column groups are not a multiple of the workgroup's 4 waves).
 void launch_gate_up_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
-void launch_gate_up_decode8(const MoeParams& p, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
-void launch_gate_up_decode16(const MoeParams& p, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_gate_up_decode8(const MoeParams& p, long waves, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_gate_up_decode16(const MoeParams& p, long waves, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 void launch_gate_up_decode4(const MoeParams& p, bool group, dim3 grid, hipStream_t stream, hipEvent_t start,
                             hipEvent_t stop);
 void launch_down_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);

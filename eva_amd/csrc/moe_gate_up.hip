@@ -19,9 +19,9 @@ void launch_gate_up_decode(const MoeParams& p, int tmax, hipStream_t stream, hip
         if (group) launch_timed(moe_gate_up_route1_kernel<true>, grid1, dim3(256), stream, start, stop, p);
         else launch_timed(moe_gate_up_route1_kernel<false>, grid1, dim3(256), stream, start, stop, p);
     } else if (tmax == 16 && group) {
-        launch_gate_up_decode16(p, grid, stream, start, stop);
+        launch_gate_up_decode16(p, waves, stream, start, stop);
     } else if (tmax >= 8 && group) {
-        launch_gate_up_decode8(p, grid, stream, start, stop);
+        launch_gate_up_decode8(p, waves, stream, start, stop);
     } else {
         launch_gate_up_decode4(p, group, grid, stream, start, stop);
     }

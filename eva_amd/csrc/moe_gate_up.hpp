@@ -97,6 +97,7 @@ template <int TM, int NW = ROT_WAVES, int CW = ROT_CW>
 struct RotStageGroup {
     static constexpr bool kWork = true;
     static constexpr int NJ = CW / NW;                 // chunks per wave and window
+    static_assert(CW % NW == 0, "a window's chunks split evenly over the waves");
     const MoeParams& p;
     const int (&so)[TM];
     int tm, w0, w1, row_words, lane, wave;
@@ -245,7 +246,7 @@ __device__ __forceinline__ void gate_up_rot_rows(const MoeParams& p, const uint3
 // (rows past tm are skipped): the kernel's register budget is its widest variant's anyway, every
 // smaller variant as well would make its compile several times longer, and every row's arithmetic
 // is the same whatever the variant (rows are independent accumulators).
-template <int K2, int TMAX, bool GROUP>
+template <int K2, int TMAX, bool GROUP, int NW = ROT_WAVES>
 __device__ __forceinline__ void gate_up_rot_fit(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                 const int* slot, int tm, int cg, int c0, int c1, float* part,
                                                 uint32_t* lds, float* lsums)
@@ -253,10 +254,10 @@ __device__ __forceinline__ void gate_up_rot_fit(const MoeParams& p, const uint32
     static_assert(TMAX == 1 || TMAX == 2 || TMAX == 4 || TMAX == 8, "decode path rows: 1, 2, 4 or 8 per unit pass");
     int so[TMAX];
     record_slots<TMAX>(slot, tm, so);
-    gate_up_rot_rows<K2, TMAX, GROUP>(p, trellis, suh, so, tm, cg, c0, c1, part, lds, lsums);
+    gate_up_rot_rows<K2, TMAX, GROUP, NW>(p, trellis, suh, so, tm, cg, c0, c1, part, lds, lsums);
 }
 
-template <int K2, int TMAX, bool GROUP>
+template <int K2, int TMAX, bool GROUP, int NW = ROT_WAVES>
 __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                  const int* slot, int rows, int cg, int c0, int c1, float* part,
                                                  uint32_t* lds, float* lsums)
@@ -266,7 +267,7 @@ __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint3
     // the GEMV is inlined once)
     for (int r0 = 0;; r0 += TMAX) {
         const int tr = rows - r0 < TMAX ? rows - r0 : TMAX;
-        gate_up_rot_fit<K2, TMAX, GROUP>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
+        gate_up_rot_fit<K2, TMAX, GROUP, NW>(p, trellis, suh, slot + r0, tr, cg, c0, c1, part, lds, lsums);
         if (r0 + TMAX >= rows) break;
         if constexpr (GROUP) __syncthreads();      // this pass's LDS reads before the next pass's writes
         else wave_lds_fence();
@@ -281,7 +282,7 @@ __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint3
 // the next unit's (two chunks of one expert, at most 16 rows) in one pass, so the expert's weights
 // are decoded once for both; the next unit's waves exit. Every row's arithmetic is that of a pass
 // of its own chunk.
-template <int K2, bool GROUP>
+template <int K2, bool GROUP, int NW>
 __device__ __forceinline__ void gate_up_rot_pair(const MoeParams& p, const uint32_t* trellis, const half_t* suh,
                                                  const UnitRec* rp, int rows, int rows_b, int cg, int c0, int c1,
                                                  float* part, uint32_t* lds, float* lsums)
@@ -290,20 +291,23 @@ __device__ __forceinline__ void gate_up_rot_pair(const MoeParams& p, const uint3
         // a unit alone: the 8-row kernel's pass
         int so[8];
         record_slots<8>(rp->slot, rows, so);
-        gate_up_rot_rows<K2, 8, GROUP>(p, trellis, suh, so, rows, cg, c0, c1, part, lds, lsums);
+        gate_up_rot_rows<K2, 8, GROUP, NW>(p, trellis, suh, so, rows, cg, c0, c1, part, lds, lsums);
         return;
     }
     int so[16];                                   // the first unit is a full chunk
     record_slots<8>(rp->slot, 8, *(int(*)[8])so);
     record_slots<8>(rp[1].slot, rows_b, *(int(*)[8])(so + 8));
-    gate_up_rot_rows<K2, 16, GROUP>(p, trellis, suh, so, 8 + rows_b, cg, c0, c1, part, lds, lsums);
+    gate_up_rot_rows<K2, 16, GROUP, NW>(p, trellis, suh, so, 8 + rows_b, cg, c0, c1, part, lds, lsums);
 }
 
-template <int TMAX, bool GROUP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_rot_kernel(MoeParams p)
+// NWG waves per workgroup; GROUP: they take NWG consecutive column groups of one (unit,
+// projection, k-split) and share its rotated rows (the column groups a multiple of NWG).
+template <int TMAX, bool GROUP, int NWG = ROT_WAVES>
+__global__ __launch_bounds__(64 * NWG) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_rot_kernel(MoeParams p)
 {
+    static_assert(GROUP || NWG == 4, "waves that rotate their own rows run four to a workgroup");
     static_assert(TMAX != 16 || GROUP, "paired units run with the workgroup's shared rows");
-    __shared__ uint32_t xl[GROUP ? 1 : 4][TMAX * rot_row_words<rot_cw<TMAX>()>()];
+    __shared__ uint32_t xl[GROUP ? 1 : NWG][TMAX * rot_row_words<rot_cw<TMAX>()>()];
     __shared__ float xsums[TMAX * rot_cw<TMAX>()];
     const int wave = threadIdx.x >> 6;
     const int wid = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
@@ -349,9 +353,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void m
 #define EVAMX_GUX(K2V)                                                                                       \
         case K2V:                                                                                            \
             if constexpr (TMAX == 16)                                                                        \
-                gate_up_rot_pair<K2V, GROUP>(p, trellis, suh, rp, rows, rows_b, cg, c0, c1, part, lds, xsums); \
+                gate_up_rot_pair<K2V, GROUP, NWG>(p, trellis, suh, rp, rows, rows_b, cg, c0, c1, part, lds, xsums); \
             else                                                                                             \
-                gate_up_rot_item<K2V, TMAX, GROUP>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); \
+                gate_up_rot_item<K2V, TMAX, GROUP, NWG>(p, trellis, suh, rp->slot, rows, cg, c0, c1, part, lds, xsums); \
             break;
         EVAMX_GUX(3) EVAMX_GUX(4) EVAMX_GUX(5) EVAMX_GUX(6) EVAMX_GUX(7) EVAMX_GUX(8) EVAMX_GUX(10)
 #undef EVAMX_GUX

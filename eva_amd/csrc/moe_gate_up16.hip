@@ -5,9 +5,14 @@
 
 namespace evamx {
 
-void launch_gate_up_decode16(const MoeParams& p, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
+void launch_gate_up_decode16(const MoeParams& p, long waves, hipStream_t stream, hipEvent_t start, hipEvent_t stop)
 {
-    launch_timed(moe_gate_up_rot_kernel<16, true>, grid, dim3(256), stream, start, stop, p);
+    // eight column groups per workgroup where they divide the column groups: each workgroup's
+    // rows are rotated once for eight column groups instead of four
+    if ((p.I / 128) % 8 == 0)
+        launch_timed(moe_gate_up_rot_kernel<16, true, 8>, dim3((unsigned)((waves + 7) / 8)), dim3(512), stream, start, stop, p);
+    else
+        launch_timed(moe_gate_up_rot_kernel<16, true, 4>, dim3((unsigned)((waves + 3) / 4)), dim3(256), stream, start, stop, p);
 }
 
 }  // namespace evamx
