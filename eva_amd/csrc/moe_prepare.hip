@@ -338,6 +338,9 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
     const ExpertLds& ex = sh.ex;
     const int n_active = ex.off[E];
     const int routed_units = ex.unit_base[E];
+    // the shared expert's units first: its chunks carry every row of the call, so its waves are
+    // among the longest, and starting them first keeps them out of the launch's last round
+    const int sh_units = p.has_shared ? expert_units(p, p.T) : 0;
     const KSplit kgu = ks_gate_up(p, p.units_max), kd = ks_down(p, p.units_max);
     for (int s = t; s < slots; s += nt) {
         const int e = sh.local[s];
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
         if (j % EVAMX_CHUNK == 0) {
             const int k2 = sh.k2[e], k2d = sh.k2d[e];
             if (!gemv_k2_supported(k2) || !gemv_k2_supported(k2d)) atomicOr(p.err, EVAMX_ERR_RATE);
-            const int ubase = ex.unit_base[e] + c * unit_mult(p, EVAMX_CHUNK);    // earlier chunks are full
+            const int ubase = sh_units + ex.unit_base[e] + c * unit_mult(p, EVAMX_CHUNK);    // earlier chunks are full
             UnitRec r;
             r.e = e;
             r.rows = rows;
@@ -391,8 +394,8 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
             for (int i = 0; i < m; ++i) p.urec[ubase + i] = r;
         }
     }
-    // the shared expert: chunks of EVAMX_CHUNK of its T rows, after the routed units
-    int n_units = routed_units;
+    // the shared expert: chunks of EVAMX_CHUNK of its T rows, units [0, sh_units)
+    const int n_units = routed_units + sh_units;
     if (p.has_shared) {
         const int nsc = (p.T + EVAMX_CHUNK - 1) / EVAMX_CHUNK;
         for (int r = t; r < p.T; r += nt) {
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
         for (int c = t; c < nsc; c += nt) {
             const int rows = min(EVAMX_CHUNK, p.T - c * EVAMX_CHUNK);
             const int m = unit_mult(p, rows);
-            const int ubase = routed_units + c * unit_mult(p, EVAMX_CHUNK);
+            const int ubase = c * unit_mult(p, EVAMX_CHUNK);
             UnitRec r;
             r.e = -1;
             r.rows = rows;
@@ -435,7 +438,6 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
             r.pad1[0] = r.pad1[1] = r.pad1[2] = 0;
             for (int i = 0; i < m; ++i) p.urec[ubase + i] = r;
         }
-        n_units += (nsc - 1) * unit_mult(p, EVAMX_CHUNK) + unit_mult(p, p.T - (nsc - 1) * EVAMX_CHUNK);
     }
     for (int u = n_units + t; u < p.units_max; u += nt) p.urec[u].e = EVAMX_NO_UNIT;
     if (t == 0) {
