@@ -264,9 +264,22 @@ struct ExpertLds {
     int chunk_base[EVAMX_MAX_EXPERTS + 1];
     int unit_base[EVAMX_MAX_EXPERTS + 1];
     int fill[EVAMX_MAX_EXPERTS];
-    int small_base[EVAMX_MAX_EXPERTS + 1];   // MFMA tiles of at most 16 rows
-    int large_base[EVAMX_MAX_EXPERTS + 1];   // MFMA tiles of more than 16 rows
+    int small_base[EVAMX_MAX_EXPERTS + 1];   // MFMA tiles of at most 16 rows (decode path: units of
+                                             // experts of more than EVAMX_CHUNK rows)
+    int large_base[EVAMX_MAX_EXPERTS + 1];   // MFMA tiles of more than 16 rows (decode path: units
+                                             // of experts of 5 to EVAMX_CHUNK rows)
 };
+
+// Decode path: the first unit of expert e when units are numbered longest first (experts of more
+// than EVAMX_CHUNK rows, then of 5 to EVAMX_CHUNK rows, then the rest; expert order within each),
+// so that the GEMV launches start their longest waves first.
+__device__ __forceinline__ int unit_order_base(const ExpertLds& ex, int E, int e)
+{
+    const int n = ex.cnt[e];
+    if (n > EVAMX_CHUNK) return ex.small_base[e];
+    if (n > 4) return ex.small_base[E] + ex.large_base[e];
+    return ex.small_base[E] + ex.large_base[E] + (ex.unit_base[e] - ex.small_base[e] - ex.large_base[e]);
+}
 
 // Work units (summed chunk weights) of an expert with n active slots.
 __device__ __forceinline__ int expert_units(const MoeParams& p, int n)
@@ -311,9 +324,16 @@ inline __device__ void expert_offsets(const MoeParams& p, ExpertLds& ex, int lan
         // MFMA tiles by size: at most 16 rows (small) or more (large); with tiles of at most 16
         // rows every tile is small, with 64-row tiles the full ones and a remainder of more
         // than 16 rows are large
+        // Decode path: the units of experts of more than EVAMX_CHUNK rows and of 5 to EVAMX_CHUNK
+        // rows (the strict prepare numbers units longest first, unit_order_base).
         const int rest = n & ((1 << cs) - 1);
-        v[4][i] = !p.mfma ? 0 : cs <= 4 ? v[2][i] : (rest > 0 && rest <= 16 ? 1 : 0);
-        v[5][i] = !p.mfma || cs <= 4 ? 0 : (n >> cs) + (rest > 16 ? 1 : 0);
+        if (p.mfma) {
+            v[4][i] = cs <= 4 ? v[2][i] : (rest > 0 && rest <= 16 ? 1 : 0);
+            v[5][i] = cs <= 4 ? 0 : (n >> cs) + (rest > 16 ? 1 : 0);
+        } else {
+            v[4][i] = n > EVAMX_CHUNK ? v[3][i] : 0;
+            v[5][i] = n > 4 && n <= EVAMX_CHUNK ? v[3][i] : 0;
+        }
 #pragma unroll
         for (int k = 0; k < 6; ++k) tot[k] += v[k][i];
     }

@@ -338,8 +338,9 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
     const ExpertLds& ex = sh.ex;
     const int n_active = ex.off[E];
     const int routed_units = ex.unit_base[E];
-    // the shared expert's units first: its chunks carry every row of the call, so its waves are
-    // among the longest, and starting them first keeps them out of the launch's last round
+    // units longest first: the shared expert's (its chunks carry every row of the call), then the
+    // routed experts' by row count (unit_order_base), so that the GEMV launches start their
+    // longest waves first and their last round holds short ones
     const int sh_units = p.has_shared ? expert_units(p, p.T) : 0;
     const KSplit kgu = ks_gate_up(p, p.units_max), kd = ks_down(p, p.units_max);
     for (int s = t; s < slots; s += nt) {
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(64 * WIDE_PREP_WAVES) void moe_prepare_wide_kernel(
         if (j % EVAMX_CHUNK == 0) {
             const int k2 = sh.k2[e], k2d = sh.k2d[e];
             if (!gemv_k2_supported(k2) || !gemv_k2_supported(k2d)) atomicOr(p.err, EVAMX_ERR_RATE);
-            const int ubase = sh_units + ex.unit_base[e] + c * unit_mult(p, EVAMX_CHUNK);    // earlier chunks are full
+            const int ubase = sh_units + unit_order_base(ex, E, e) + c * unit_mult(p, EVAMX_CHUNK);    // earlier chunks are full
             UnitRec r;
             r.e = e;
             r.rows = rows;
