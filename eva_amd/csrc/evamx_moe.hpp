@@ -44,7 +44,7 @@ struct alignas(128) UnitRec {
     int ubase;                  // first unit of the chunk (a chunk of weight m owns m units)
     int s_gu, s_d;              // k-splits of the chunk's gate/up and down GEMVs
     int k2_d;                   // 2 x bits of down
-    int pair;                   // gate/up of strict calls: 1 this unit's waves take the next unit's
+    int pair;                   // GEMVs of strict calls: 1 this unit's waves take the next unit's
                                 // rows too (same expert), -1 the previous unit's take these, 0 alone
     int slot[EVAMX_CHUNK];      // the chunk's slots (entries past rows repeat slot[0])
     uint64_t tr[3];             // gate, up, down trellis
@@ -164,11 +164,11 @@ __host__ __device__ __forceinline__ int chunk_mult(int rows) { return rows <= 3 
 __host__ __device__ __forceinline__ int unit_mult(const MoeParams& p, int rows) { return p.strict ? 1 : chunk_mult(rows); }
 
 // Strict calls of more than EVAMX_CHUNK rows pair each expert's chunks (2c, 2c + 1) for the gate/up
-// launch: one wave decodes the expert's weights once for both chunks' rows (at most 16). The gate/up
-// kernel for them runs workgroups of four column groups (I / 128 a multiple of 4).
+// and down launches: one wave decodes the expert's weights once for both chunks' rows (at most 16).
+// Their kernels run workgroups of four (or eight) column groups (I / 128 and H / 128 multiples of 4).
 __host__ __device__ __forceinline__ bool pair_units(const MoeParams& p)
 {
-    return p.strict && p.T > EVAMX_CHUNK && (p.I / 128) % 4 == 0;
+    return p.strict && p.T > EVAMX_CHUNK && (p.I / 128) % 4 == 0 && (p.H / 128) % 4 == 0;
 }
 // UnitRec::pair of chunk c of nch chunks of one expert.
 __host__ __device__ __forceinline__ int unit_pair(int c, int nch) { return (c & 1) ? -1 : (c + 1 < nch ? 1 : 0); }
@@ -254,6 +254,7 @@ void launch_gate_up_decode16(const MoeParams& p, long waves, hipStream_t stream,
 void launch_gate_up_decode4(const MoeParams& p, bool group, dim3 grid, hipStream_t stream, hipEvent_t start,
                             hipEvent_t stop);
 void launch_down_decode(const MoeParams& p, int tmax, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+void launch_down_decode16(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 void launch_act(const MoeParams& p, int nslot, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 void launch_act_class(const MoeParams& p, int cls, hipStream_t stream);
 void launch_combine(const MoeParams& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop);

@@ -92,11 +92,13 @@ int moe_launch(MoeParams& p, hipStream_t stream, void* const* events)
         // passes, and a chunk with more rows than the pass (given routes that repeat an expert)
         // runs in several.
         const int tmax = p.T <= 1 ? 1 : p.T <= 2 ? 2 : 8;
-        // strict calls of more than 8 rows: gate/up takes an expert's chunks in pairs (its
-        // weights decoded once for up to 16 rows)
-        launch_gate_up_decode(p, pair_units(p) ? 16 : tmax, stream, ev(2), ev(3));
+        // strict calls of more than 8 rows: gate/up and down take an expert's chunks in pairs
+        // (its weights decoded once for up to 16 rows)
+        const bool pairs = pair_units(p);
+        launch_gate_up_decode(p, pairs ? 16 : tmax, stream, ev(2), ev(3));
         launch_act(p, nslot, stream, ev(4), ev(5));
-        launch_down_decode(p, tmax, stream, ev(6), ev(7));
+        if (pairs) launch_down_decode16(p, stream, ev(6), ev(7));
+        else launch_down_decode(p, tmax, stream, ev(6), ev(7));
     }
     launch_combine(p, stream, ev(8), ev(9));
     return hipGetLastError() == hipSuccess ? 0 : -1;
