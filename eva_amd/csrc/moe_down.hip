@@ -1,6 +1,6 @@
-// Down launch of the decode path (calls of 1-2 rows, and strict calls of up to 8 rows); the
-// kernels sit in moe_down.hpp, the paired-chunk kernel of strict calls of more than 8 rows in
-// moe_down16.hip.
+// Down launch of the decode path for calls of 1-2 rows (and of more where the column groups are
+// not a multiple of 4); the kernels sit in moe_down.hpp, the workgroup-staged kernel of strict calls
+// of more than 2 rows in moe_down16.hip.
 #include "moe_down.hpp"
 
 namespace evamx {

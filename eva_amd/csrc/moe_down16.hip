@@ -1,6 +1,7 @@
-// Down launch of strict calls of more than 8 rows, with each expert's 8-row chunks paired as in
-// gate/up (UnitRec::pair): the first unit's waves take both chunks' rows (up to 16, four MFMA row
-// groups), so the expert's weights are decoded once for both; the second unit's waves exit. The
+// Down launch of strict calls of more than 2 rows. In calls of more than 8 rows each expert's 8-row
+// chunks are paired as in gate/up (UnitRec::pair): the first unit's waves take both chunks' rows (up
+// to 16, four MFMA row groups), so the expert's weights are decoded once for both; the second unit's
+// waves exit. The
 // four waves of a workgroup take four consecutive column groups of one (unit, k-split) and stage
 // its activation rows into LDS once for all four (16 rows per wave would leave LDS for fewer
 // waves). Every row's arithmetic is that of moe_down_rec_kernel's pass of its own chunk.
