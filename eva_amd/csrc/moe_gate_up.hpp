@@ -85,9 +85,10 @@ struct RotStage {
     }
 };
 
-// The same rotations shared by the four waves of a workgroup, which then stream four column
-// groups of the same (unit, projection, k-split): wave w rotates chunks w, w + 4, ... of the
-// window (CW chunks at most) into the workgroup's LDS rows and stores each chunk's sum. After a
+// The same rotations shared by the NW waves of a workgroup (four, or eight in the strict kernels),
+// which then stream NW column groups of the same (unit, projection, k-split): wave w rotates chunks
+// w, w + NW, ... of the window (CW chunks at most) into the workgroup's LDS rows and stores each
+// chunk's sum. After a
 // barrier the rows are ready; add_sums() adds a row's chunk sums in chunk order (the order of the
 // per-wave stage, so the results are the same), after the GEMV so that the sums hold no
 // registers during it. The rows' x words load through one resource with per-row scalar offsets.
@@ -174,7 +175,7 @@ constexpr int rot_row_words() { return CW * 64 + 8; }
 constexpr int ROT_ROW_WORDS = rot_row_words<ROT_CW>();
 
 // Gate/up GEMV of tm rows (slots slot[0..tm)) over the 128-chunks [c0, c1): each window of at
-// most rot_cw<TM>() chunks is rotated into LDS (GROUP: by the workgroup's four waves together),
+// most rot_cw<TM>() chunks is rotated into LDS (GROUP: by the workgroup's NW waves together),
 // then streamed with the products on the matrix cores (gemv_wave_m4, rows in groups of four);
 // writes the fp32 partials of the rows.
 template <int K2, int TM, bool GROUP, int NW = ROT_WAVES>
@@ -274,10 +275,6 @@ __device__ __forceinline__ void gate_up_rot_item(const MoeParams& p, const uint3
     }
 }
 
-// One wave per (unit, gate|up, k-split, 128 columns). GROUP (the column-group count a multiple
-// of 4): the items run column group fastest, so the four waves of a workgroup share unit,
-// projection and k-split (and exit together) and rotate their inputs together; otherwise every
-// wave rotates its own.
 // Paired units (TMAX 16, strict calls): a unit whose record says pair > 0 takes its own rows and
 // the next unit's (two chunks of one expert, at most 16 rows) in one pass, so the expert's weights
 // are decoded once for both; the next unit's waves exit. Every row's arithmetic is that of a pass
@@ -300,8 +297,10 @@ __device__ __forceinline__ void gate_up_rot_pair(const MoeParams& p, const uint3
     gate_up_rot_rows<K2, 16, GROUP, NW>(p, trellis, suh, so, 8 + rows_b, cg, c0, c1, part, lds, lsums);
 }
 
-// NWG waves per workgroup; GROUP: they take NWG consecutive column groups of one (unit,
-// projection, k-split) and share its rotated rows (the column groups a multiple of NWG).
+// One wave per (unit, gate|up, k-split, 128 columns), NWG waves per workgroup. GROUP (the
+// column-group count a multiple of NWG): the items run column group fastest, so the waves of a
+// workgroup share unit, projection and k-split (and exit together) and rotate their inputs
+// together; otherwise every wave rotates its own (four waves per workgroup).
 template <int TMAX, bool GROUP, int NWG = ROT_WAVES>
 __global__ __launch_bounds__(64 * NWG) __attribute__((amdgpu_waves_per_eu(4))) void moe_gate_up_rot_kernel(MoeParams p)
 {
