@@ -240,12 +240,14 @@ def test_strict_router_front_no_shared(dev):
     assert int(ws.flags().cpu()[0]) == 0
 
 
-def test_strict_graph_replays(dev):
-    """A strict 8-token call (wide prepare, 8-row kernels) captured into a graph: three replays,
-    with eager calls of other sizes in between, each bit-identical to the eager call."""
+@pytest.mark.parametrize("H, T", [(256, 8), (512, 16)])
+def test_strict_graph_replays(dev, H, T):
+    """A strict 8-token call (wide prepare, 8-row kernels) and a 16-token one at H = I = 512 (paired
+    chunks, workgroup-staged down) captured into a graph: three replays, with eager calls of other
+    sizes in between, each bit-identical to the eager call."""
     ops = _ops()
-    H, I, E, topk, T = 256, 512, 16, 8, 8
-    rng = np.random.default_rng(78)
+    I, E, topk = 512, 16, 8
+    rng = np.random.default_rng(78 + T)
     experts, shared = _small_case(rng, H, I, E)
     de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
     x = to_dev(synth.activations_bf16(rng, T, H), dev).to(torch.bfloat16)
@@ -267,7 +269,7 @@ def test_strict_graph_replays(dev):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         call(T)
-    for n in (3, 5, 1):
+    for n in (3, 5, 1, T - 2):
         out.zero_()
         call(n)                                          # eager work of another size in between
         torch.cuda.synchronize()
