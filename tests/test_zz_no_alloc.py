@@ -151,19 +151,15 @@ def test_static_refusals(dev, case):
     assert L.evamx_moe_forward_static(ctypes.byref(a), None) == _lib.EVAMX_EINVAL
 
 
-def test_static_strict_rows(dev, case):
-    """Strict mode on the fixed scratch: a 16-row static call with strict_rows 16 gives the bits of
-    the workspace path in strict mode, and each of its rows the bits of a one-row static call (the
-    strict property), then an 8-row call the bits of its own rows alone."""
+def _strict_static(dev, de, ds, inter, seed):
     from eva_amd import ops
-    experts, shared, de, ds = case
-    rng = np.random.default_rng(812)
+    rng = np.random.default_rng(seed)
     kw = dict(limit=0.75, bits=4, shared_ptrs=ds.ptrs(0), shared_bits=4)
 
     def static(x, z, strict_rows):
         rows = x.shape[0]
         out = torch.empty(rows, H, dtype=torch.float32, device=dev)
-        ops.moe_forward_static(ops.MoeShape(ROWS_MAX, H, I, TOPK, E, 1, 0, 0, strict_rows), x, de.table, out,
+        ops.moe_forward_static(ops.MoeShape(ROWS_MAX, H, inter, TOPK, E, 1, 0, 0, strict_rows), x, de.table, out,
                                logits=z, sel=torch.empty(rows, TOPK, dtype=torch.int64, device=dev),
                                weights=torch.empty(rows, TOPK, dtype=torch.float32, device=dev), **kw)
         torch.cuda.synchronize()
@@ -173,7 +169,7 @@ def test_static_strict_rows(dev, case):
         x = to_dev(synth.activations_bf16(rng, rows, H), dev).to(torch.bfloat16)
         z = to_dev(synth.logits_skewed(rng, rows, E, hot=1, warm=3), dev)
         got = static(x, z, ROWS_MAX)
-        ws = ops.MoeWorkspace(dev, rows_max=ROWS_MAX, hidden=H, inter=I, topk=TOPK, n_local=E, has_shared=True,
+        ws = ops.MoeWorkspace(dev, rows_max=ROWS_MAX, hidden=H, inter=inter, topk=TOPK, n_local=E, has_shared=True,
                               strict_rows=ROWS_MAX)
         want = torch.empty_like(got)
         ops.moe_forward(ws, x, de.table, want, logits=z, sel=torch.empty(rows, TOPK, dtype=torch.int64, device=dev),
@@ -183,3 +179,20 @@ def test_static_strict_rows(dev, case):
         for r in range(rows):
             alone = static(x[r:r + 1], z[r:r + 1], ROWS_MAX)
             assert torch.equal(alone.view(torch.int32), got[r:r + 1].view(torch.int32)), (rows, r)
+
+
+def test_static_strict_rows(dev, case):
+    """Strict mode on the fixed scratch: a 16-row static call with strict_rows 16 gives the bits of
+    the workspace path in strict mode, and each of its rows the bits of a one-row static call (the
+    strict property), then an 8-row call the bits of its own rows alone."""
+    experts, shared, de, ds = case
+    _strict_static(dev, de, ds, I, 812)
+
+
+def test_static_strict_rows_paired_chunks(dev):
+    """The same at I = 512 (four column groups), where the 16-row call pairs each expert's 8-row
+    chunks (the hot expert's 16 rows and the shared expert's) in gate/up and down."""
+    rng = np.random.default_rng(813)
+    experts = [synth.expert(rng, H, 512, 4, 1 / np.sqrt(H)) for _ in range(E)]
+    shared = synth.expert(rng, H, 512, 4, 1 / np.sqrt(H))
+    _strict_static(dev, DeviceExperts(experts, dev), DeviceExperts([shared], dev), 512, 814)
