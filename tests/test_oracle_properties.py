@@ -3,7 +3,7 @@ seeded cases may miss (empty calls, one expert, repeated and out-of-range expert
 weights, ties, signed zeros, subnormals, infinities). Each property is stated independently of
 the oracle's own code: the run table against the run-cutting rules (`_check_table`), the top-k
 against Python's sort on (key desc, index asc), the Hadamard against its algebra, and the bf16 /
-fp16 roundings against torch's and numpy's casts."""
+fp16 roundings against torch's casts."""
 import numpy as np
 import pytest
 import torch
@@ -38,7 +38,7 @@ def test_run_table_rules(r):
     weights inactive, an expert range or none, an empty call)."""
     sel, rw, cap, lo, hi = r
     if lo < 0:
-        # without an expert range every non-negative id below the table's experts is a local one
+        # without an expert range every non-negative id is a local expert
         sel = np.abs(sel)
         table = coop.reference_table(sel, rw, cap)
         _check_table(sel, rw, table, cap)
