@@ -98,20 +98,29 @@ def _small_case(rng, H, I, E, rates=None, down_rates=None, shared_down=None):
 
 
 @pytest.mark.parametrize("H, I", [(256, 512), (256, 384), (512, 512)])
-@pytest.mark.parametrize("case", ["routed", "mixed_gated", "given_repeats"])
+@pytest.mark.parametrize("case", ["routed", "mixed_gated", "given_repeats", "other_rates"])
 def test_strict_small_shapes_bit_identical(dev, H, I, case):
     """Reduced shapes, up to 32 tokens (256 slots, the strict bound): every row of calls of 2, 3, 5,
     8, 13, 20 and 32 tokens equals the row alone, bit for bit, and the oracle within the tolerance.
     I = 384 (3 column groups of gate/up) takes the 2-row-pass kernel, I = 512 the 8-row one. At
     H = I = 512 (four column groups of each) calls of more than 8 tokens pair each expert's 8-row
     chunks in gate/up and down (up to 16 rows per pass; the expert picked twice by every token in
-    given_repeats has 64 slots, four pairs), and down runs the workgroup-staged kernel from 3 tokens."""
+    given_repeats has 64 slots, four pairs), and down runs the workgroup-staged kernel from 3 tokens.
+    mixed_gated and other_rates together run every gate/up and down rate of the decode path."""
     ops = _ops()
     E, topk, rows = 24, 8, 32
-    rng = np.random.default_rng({"routed": 1, "mixed_gated": 2, "given_repeats": 3}[case] * 100 + I + (H - 256))
+    rng = np.random.default_rng({"routed": 1, "mixed_gated": 2, "given_repeats": 3, "other_rates": 4}[case] * 100 + I
+                                + (H - 256))
     kw, ref_kw = {}, {}
     x = synth.activations_bf16(rng, rows, H)
-    if case == "mixed_gated":
+    if case == "other_rates":
+        # the rates mixed_gated leaves out: gate/up 1.5, 3.5 and 5 bpw, down 1.5, 2, 2.5 and 3.5
+        rates = synth.mixed_rates(rng, E, (1.5, 3.5, 5))
+        drates = synth.mixed_rates(rng, E, (1.5, 2, 2.5, 3.5))
+        experts, shared = _small_case(rng, H, I, E, rates, drates, shared_down=2.5)
+        de, ds = DeviceExperts(experts, dev), DeviceExperts([shared], dev)
+        kw = dict(k2_per_expert=de.k2, k2_down_per_expert=de.k2_down, shared_bits_down=2.5)
+    elif case == "mixed_gated":
         rates = synth.mixed_rates(rng, E, (2, 2.5, 3, 4))
         drates = synth.mixed_rates(rng, E, (3, 4, 5))
         experts, shared = _small_case(rng, H, I, E, rates, drates, shared_down=4.0)
