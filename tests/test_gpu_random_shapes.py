@@ -6,7 +6,8 @@ and the two-class prefill pipeline).
 
 Each case: routes bit-exact against the oracle's top-k, layer output within the oracle's 1e-2
 row-relative tolerance, no flag raised; in strict mode every row also equals its one-row call bit
-for bit."""
+for bit. The single EXL3 linear likewise, over random widths (1 to 40 chunks of 128 in, 1 to 10
+out), rates and row counts on both sides of its 16-row switch to the MFMA tiles."""
 import numpy as np
 import pytest
 import torch
@@ -82,3 +83,21 @@ def test_random_layer_configuration(dev, seed):
     if c["strict"] and rows > 1:
         y1 = np.concatenate([run(r, 1)[0] for r in range(rows)])
         assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_linear_configuration(dev, seed):
+    from eva_amd import ops
+    rng = np.random.default_rng(9300 + seed)
+    n_in = 128 * int(rng.choice([1, 3, 5, 9, 16, 40]))
+    n_out = 128 * int(rng.choice([1, 3, 5, 7, 10]))
+    rows = int(rng.choice([1, 2, 3, 9, 16, 17, 50]))
+    K = float(rng.choice(RATES))
+    print("case", seed, dict(n_in=n_in, n_out=n_out, rows=rows, K=K), flush=True)
+    tr, suh, svh = synth.projection(rng, n_in, n_out, K, svh_scale=1 / np.sqrt(n_in))
+    x = rng.standard_normal((rows, n_in)).astype(np.float16)
+    ws = torch.full((ops.lib().evamx_exl3_linear_workspace_bytes(rows, n_in, n_out),), 0x5a, dtype=torch.uint8,
+                    device=dev)
+    y = ops.exl3_linear(to_dev(x, dev), to_dev(tr, dev), to_dev(suh, dev), to_dev(svh, dev), K, workspace=ws)
+    ref = coop.exl3_linear(x, tr, suh, svh, K)
+    assert rel_err_rows(y.cpu().numpy().astype(np.float32), ref.astype(np.float32)) < TOL
