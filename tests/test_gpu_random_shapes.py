@@ -6,7 +6,8 @@ and the two-class prefill pipeline).
 
 Each case: routes bit-exact against the oracle's top-k, layer output within the oracle's 1e-2
 row-relative tolerance, no flag raised; in strict mode every row also equals its one-row call bit
-for bit. The single EXL3 linear likewise, over random widths (1 to 40 chunks of 128 in, 1 to 10
+for bit. Given routes likewise, with an expert range (ids outside it inactive), experts repeated
+within a token, zero weights and fp32 or fp16 weights. The single EXL3 linear likewise, over random widths (1 to 40 chunks of 128 in, 1 to 10
 out), rates and row counts on both sides of its 16-row switch to the MFMA tiles."""
 import numpy as np
 import pytest
@@ -82,6 +83,60 @@ def test_random_layer_configuration(dev, seed):
     assert rel_err_rows(y, ref) < TOL
     if c["strict"] and rows > 1:
         y1 = np.concatenate([run(r, 1)[0] for r in range(rows)])
+        assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_given_routes(dev, seed):
+    from eva_amd import ops
+    rng, c = _draw(100 + seed)
+    H, I, E, topk, rows = c["H"], c["I"], c["E"], c["topk"], c["rows"]
+    lo = int(rng.integers(0, 20))
+    hi = lo + E
+    experts = [synth.expert(rng, H, I, float(rng.choice(RATES)), 1 / np.sqrt(H), K_down=float(rng.choice(RATES)))
+               for _ in range(E)]
+    shared = synth.expert(rng, H, I, 3.0, 1 / np.sqrt(H)) if c["has_shared"] else None
+    x = synth.activations_bf16(rng, rows, H)
+    sel = rng.integers(lo - 3, hi + 3, size=(rows, topk)).astype(np.int64)     # some outside the range
+    if topk > 1 and rng.random() < 0.5:
+        sel[:, rng.integers(0, topk)] = sel[0, 0] if lo <= sel[0, 0] < hi else lo   # one expert repeated
+    w = rng.uniform(0.05, 1.0, size=(rows, topk)).astype(np.float32)
+    w[rng.random((rows, topk)) < 0.15] = 0.0
+    rw = w.astype(np.float16)
+    xh = x.astype(np.float32).astype(np.float16)
+    ref = coop.moe_routed(xh, sel, rw, dict(enumerate(experts)), c["limit"], min_expert=lo, max_expert=hi)
+    if shared is not None:
+        ref = ref + coop.shared_expert(xh, shared, c["limit"])
+    ref = np.asarray(ref, np.float32)
+
+    de = DeviceExperts(experts, dev)
+    kw = dict(k2_per_expert=de.k2, k2_down_per_expert=de.k2_down, min_expert=lo, max_expert=hi)
+    if shared is not None:
+        ds = DeviceExperts([shared], dev)
+        kw.update(shared_ptrs=ds.ptrs(0), shared_bits=3.0)
+    ws = ops.MoeWorkspace(dev, rows_max=rows, hidden=H, inter=I, topk=topk, n_local=E, has_shared=shared is not None,
+                          strict_rows=rows if c["strict"] else 0)
+    ws.buffer.fill_(0xa5)
+    ws.clear_flags()
+    xd = to_dev(x, dev).to(torch.bfloat16)
+    sd = to_dev(sel, dev)
+    half = bool(rng.random() < 0.5)
+    wd = to_dev(rw if half else w, dev)
+
+    def run(r0, T):
+        out = torch.empty(T, H, dtype=torch.float32, device=dev)
+        wk = {"rw" if half else "weights": wd[r0:r0 + T].contiguous()}
+        ops.moe_forward(ws, xd[r0:r0 + T], de.table, out, limit=c["limit"], sel=sd[r0:r0 + T].contiguous(), **wk,
+                        **kw)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    print("case", seed, c, dict(lo=lo, hi=hi, half=half), flush=True)
+    y = run(0, rows)
+    assert int(ws.flags().cpu()[0]) == 0
+    assert rel_err_rows(y, ref) < TOL
+    if c["strict"] and rows > 1:
+        y1 = np.concatenate([run(r, 1) for r in range(rows)])
         assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
 
 
