@@ -7,7 +7,8 @@ and the two-class prefill pipeline).
 Each case: routes bit-exact against the oracle's top-k, layer output within the oracle's 1e-2
 row-relative tolerance, no flag raised; in strict mode every row also equals its one-row call bit
 for bit. Given routes likewise, with an expert range (ids outside it inactive), experts repeated
-within a token, zero weights and fp32 or fp16 weights. The single EXL3 linear likewise, over random widths (1 to 40 chunks of 128 in, 1 to 10
+within a token, zero weights and fp32 or fp16 weights. Captured into a hipGraph, each replay with new
+inputs equals the eager call bit for bit. The single EXL3 linear likewise, over random widths (1 to 40 chunks of 128 in, 1 to 10
 out), rates and row counts on both sides of its 16-row switch to the MFMA tiles."""
 import numpy as np
 import pytest
@@ -138,6 +139,54 @@ def test_random_given_routes(dev, seed):
     if c["strict"] and rows > 1:
         y1 = np.concatenate([run(r, 1) for r in range(rows)])
         assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_graph_replays(dev, seed):
+    from eva_amd import ops
+    rng, c = _draw(200 + seed)
+    H, I, E, topk, T = c["H"], c["I"], c["E"], c["topk"], c["rows"]
+    experts = [synth.expert(rng, H, I, float(rng.choice(RATES)), 1 / np.sqrt(H), K_down=float(rng.choice(RATES)))
+               for _ in range(E)]
+    shared = synth.expert(rng, H, I, 4.0, 1 / np.sqrt(H)) if c["has_shared"] else None
+    de = DeviceExperts(experts, dev)
+    kw = dict(k2_per_expert=de.k2, k2_down_per_expert=de.k2_down)
+    if shared is not None:
+        ds = DeviceExperts([shared], dev)
+        kw.update(shared_ptrs=ds.ptrs(0), shared_bits=4.0)
+    ws = ops.MoeWorkspace(dev, rows_max=T, hidden=H, inter=I, topk=topk, n_local=E, has_shared=shared is not None,
+                          strict_rows=T if c["strict"] else 0)
+    xs = torch.zeros(T, H, dtype=torch.bfloat16, device=dev)
+    zs = torch.zeros(T, E, dtype=torch.float32, device=dev)
+    sel = torch.empty(T, topk, dtype=torch.int64, device=dev)
+    w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    out = torch.empty(T, H, dtype=torch.float32, device=dev)
+
+    def fwd():
+        ops.moe_forward(ws, xs, de.table, out, limit=c["limit"], logits=zs, sel=sel, weights=w, **kw)
+
+    print("case", seed, c, flush=True)
+    fwd()                                        # outside capture first (a call of more than 16 tokens makes its side stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        x = synth.activations_bf16(rng, T, H)
+        z = synth.logits_zipf(rng, T, E)
+        xs.copy_(to_dev(x, dev).to(torch.bfloat16))
+        zs.copy_(to_dev(z, dev))
+        graph.replay()
+        torch.cuda.synchronize()
+        y_graph, idx_graph = out.clone(), sel.clone()
+        fwd()                                    # eager on the same inputs
+        torch.cuda.synchronize()
+        assert torch.equal(idx_graph, sel), rep
+        assert torch.equal(y_graph, out), rep
+        ref, ridx, _, _ = coop.moe_layer(x, z, experts, shared, topk, c["limit"])
+        assert np.array_equal(idx_graph.cpu().numpy(), ridx)
+        assert rel_err_rows(y_graph.cpu().numpy(), ref) < TOL
 
 
 @pytest.mark.parametrize("seed", range(24))
