@@ -196,3 +196,50 @@ def test_static_strict_rows_paired_chunks(dev):
     experts = [synth.expert(rng, H, 512, 4, 1 / np.sqrt(H)) for _ in range(E)]
     shared = synth.expert(rng, H, 512, 4, 1 / np.sqrt(H))
     _strict_static(dev, DeviceExperts(experts, dev), DeviceExperts([shared], dev), 512, 814)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_static_random_configurations(dev, seed):
+    """Seeded random shapes (widths of 2-8 chunks of 128, any expert count and top-k, mixed gate/up
+    and down rates, a shared expert or none, strict or automatic geometry): two calls in a row on
+    the fixed scratch, the second with fewer rows, each bit-identical to the workspace path."""
+    from eva_amd import ops
+    rng = np.random.default_rng(820 + seed)
+    h, i = 128 * int(rng.integers(2, 9)), 128 * int(rng.integers(2, 9))
+    e = int(rng.integers(4, 33))
+    k = int(rng.integers(1, min(8, e) + 1))
+    rows_max = int(rng.choice([2, 5, 16, 24, 40]))
+    strict = rows_max if rows_max * k <= 256 and rng.random() < 0.5 else 0
+    has_shared = bool(rng.random() < 0.7)
+    rates = (1.5, 2, 2.5, 3, 3.5, 4, 5)
+    experts = [synth.expert(rng, h, i, float(rng.choice(rates)), 1 / np.sqrt(h), K_down=float(rng.choice(rates)))
+               for _ in range(e)]
+    de = DeviceExperts(experts, dev)
+    kw = dict(limit=10.0, k2_per_expert=de.k2, k2_down_per_expert=de.k2_down)
+    if has_shared:
+        ds = DeviceExperts([synth.expert(rng, h, i, 3.0, 1 / np.sqrt(h))], dev)
+        kw.update(shared_ptrs=ds.ptrs(0), shared_bits=3.0)
+    shape = ops.MoeShape(rows_max, h, i, k, e, int(has_shared), 0, 0, strict)
+    print("case", seed, dict(h=h, i=i, e=e, k=k, rows_max=rows_max, strict=strict, shared=has_shared), flush=True)
+    for n, rows in enumerate((rows_max, max(1, rows_max // 3))):
+        x = to_dev(synth.activations_bf16(rng, rows, h), dev).to(torch.bfloat16)
+        z = to_dev(synth.logits_zipf(rng, rows, e), dev)
+        res = []
+        for static in (True, False):
+            sel = torch.full((rows, k), -1, dtype=torch.int64, device=dev)
+            w = torch.full((rows, k), -1.0, dtype=torch.float32, device=dev)
+            out = torch.full((rows, h), float("nan"), dtype=torch.float32, device=dev)
+            if static:
+                ops.moe_forward_static(shape, x, de.table, out, logits=z, sel=sel, weights=w, **kw)
+            else:
+                ws = ops.MoeWorkspace(dev, rows_max=rows_max, hidden=h, inter=i, topk=k, n_local=e,
+                                      has_shared=has_shared, strict_rows=strict)
+                ws.buffer.fill_(0x7f)
+                ws.clear_flags()
+                ops.moe_forward(ws, x, de.table, out, logits=z, sel=sel, weights=w, **kw)
+            torch.cuda.synchronize()
+            res.append((out.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()))
+        for g, want in zip(*res):
+            assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
+                                  want.view(np.uint32) if want.dtype == np.float32 else want), (n, rows)
+        assert np.isfinite(res[0][0]).all()
